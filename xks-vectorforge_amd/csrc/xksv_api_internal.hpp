@@ -1,0 +1,32 @@
+// Internal declarations shared by the host translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <vector>
+
+#include "../../include/xksv_hip.h"
+#include "xksv_shared.hpp"
+
+namespace xksv {
+
+struct SlabSpec {
+  uint64_t offset, length, rows, cols;  // rows == 0: raw slab
+};
+
+bool encode_serial(const uint8_t* data, uint64_t rows, uint64_t cols, std::vector<uint8_t>& v);
+bool encode_parallel(const uint8_t* data, uint64_t rows, uint64_t cols, std::vector<uint8_t>& v);
+std::vector<SlabSpec> slab_rule(uint64_t nbytes, bool bf16, uint64_t shape_cols);
+
+// Kernel launchers (xksv_kernels.hip).  max_groups bounds the persistent grid.
+hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc, uint8_t* out,
+                         uint32_t* status, unsigned max_groups, hipStream_t s);
+hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
+                           const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
+                           float* partial, uint32_t* counters, unsigned max_groups, hipStream_t s);
+hipError_t launch_copy_raw(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint8_t* out, hipStream_t s);
+hipError_t launch_gemm_plain(const DevBlock* blocks, uint32_t nblocks, const uint8_t* base, const float* x,
+                             uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, hipStream_t s);
+hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t s);
+
+}  // namespace xksv

@@ -1,0 +1,46 @@
+// Types shared by the host API (xksv_api.cpp) and the gfx950 kernels
+// (xksv_kernels.hip).  Plain structs only: no torch types, no STL.
+#pragma once
+#include <stdint.h>
+
+namespace xksv {
+
+// Block codecs, as named in the archive index (src/compile.cpp:266-268).
+enum Codec : uint32_t {
+  kCodecRaw = 0,       // "raw": original bytes
+  kCodecSerial = 1,    // "bf16-huffman-tile16": one Huffman stream per slab
+  kCodecParallel = 2,  // "bf16-huffman-parallel32": XKSP2 block, <= 32 substreams
+};
+
+// Per-block error bits written to the status array (0 = block decoded).
+enum Err : uint32_t {
+  kErrHeader = 1,    // block or substream header fails the reference's validation
+  kErrCodebook = 2,  // oversubscribed canonical code lengths
+  kErrStream = 4,    // invalid code, truncated stream, trailing bits, or count mismatch
+  kErrShape = 8,     // header shape disagrees with the descriptor, or exceeds device limits
+};
+
+// One encoded block as the kernels see it (device memory).  `src` and `size`
+// locate the encoded bytes inside the archive buffer; `dst` is the output byte
+// offset (decode) or the first output row (GEMV/GEMM).  `rows`/`cols` are the
+// index's slab shape (src/compile.cpp:461-468).
+struct DevBlock {
+  uint64_t src;
+  uint64_t size;
+  uint64_t dst;
+  uint64_t rows;
+  uint64_t cols;
+  uint32_t codec;
+  uint32_t status_slot;  // index into the status array
+};
+
+// Device element limit per block: element indices are 32-bit in the kernels.
+constexpr uint64_t kMaxBlockElems = (1ull << 31) - 1;
+// Partial-sum slots per parallel block for the deterministic cross-substream
+// reduction of the fused GEMV (one per substream).
+constexpr uint32_t kMaxChunks = 32;
+// Largest batch one fused GEMM launch handles in registers; larger batches
+// are split into column groups by the host.
+constexpr uint32_t kMaxFusedBatch = 16;
+
+}  // namespace xksv
