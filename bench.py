@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Benchmark of the XKSV compressed-weight hot path on one MI355X.
+
+Workload (the headline): whole-archive decode of a Llama-3-8B-shaped BF16
+archive compiled with dfloat11-parallel (XKSP2 parallel32 blocks): 32 layers
+of q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096,
+down 4096x14336, two RMSNorm vectors 1+N(0, 0.05), plus a 128256x4096
+embedding; weights N(0, 0.02) from per-tensor seeds (synthetic data, random
+init).  7,504,924,672 elements, 15.0 GB of BF16.  One step = one decode of
+every block of the archive (resident in HBM) into BF16 in HBM, through the
+device-resident plan API of libxksv_hip.so.
+
+`value` = decoded BF16 GB/s (rows*cols*2 bytes per step / step time).
+Also reported: roofline fraction of the decode launch (encoded bytes read +
+BF16 bytes written, per launch, over the launch time measured with HIP
+events), the fused batch-1 decode-GEMV time per layer at 14336x4096 and
+4096x14336 (rotating over 16 resident copies so the 256 MB last-level cache
+cannot serve repeats), a plain device copy's GB/s, and the reference CPU
+decode (the reference's own codec compiled from source, oracle/_ref) timed on
+this host's cores on a bounded sample of the same archive.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "xks-vectorforge_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decoded BF16 GB/s + % HBM peak; fused decode-GEMV µs/layer at 14336x4096"
+LAYER = [("q_proj", (4096, 4096)), ("k_proj", (1024, 4096)), ("v_proj", (1024, 4096)), ("o_proj", (4096, 4096)),
+         ("gate_proj", (14336, 4096)), ("up_proj", (14336, 4096)), ("down_proj", (4096, 14336)),
+         ("input_layernorm", (4096,)), ("post_attention_layernorm", (4096,))]
+EMBED = ("embed_tokens", (128256, 4096))
+
+
+def log(msg: str) -> None:
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def gen_bf16(torch, shape, seed: int, norm: bool):
+    """N(0, 0.02) weights (or 1 + N(0, 0.05) norm vectors) as BF16 on the GPU, seeded per tensor."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+    x = x.mul_(0.05).add_(1.0) if norm else x.mul_(0.02)
+    return x.to(torch.bfloat16)
+
+
+def build_archive(torch, lib, layers: int, codec: int):
+    """Generate, encode (host threads, the compiler's slab rule) and upload the archive."""
+    import xksv_hip
+    tensors = [EMBED] + [(f"layers.{i}.{n}", s) for i in range(layers) for n, s in LAYER]
+    encs, tables, meta = [], [], []
+    arc_off = out_off = 0
+    t0 = time.time()
+    for idx, (name, shape) in enumerate(tensors):
+        w = gen_bf16(torch, shape, 1000 + idx, name.endswith("norm"))
+        words = w.view(torch.int16).cpu().numpy().view(np.uint16)
+        enc, table = lib.encode_tensor(words, codec)
+        table = table.copy()
+        table["offset"] += arc_off
+        table["out_offset"] += out_off
+        encs.append(enc)
+        tables.append(table)
+        meta.append((name, shape, 1000 + idx, out_off, words.nbytes))
+        arc_off += enc.nbytes
+        out_off += words.nbytes
+        if idx % 40 == 0:
+            log(f"encoded {idx + 1}/{len(tensors)} tensors, {out_off / 1e9:.1f} GB raw, {time.time() - t0:.0f}s")
+    table = np.concatenate(tables)
+    d_arc = torch.empty(arc_off, dtype=torch.uint8, device="cuda")
+    pos = 0
+    for e in encs:
+        d_arc[pos:pos + e.nbytes].copy_(torch.from_numpy(e))
+        pos += e.nbytes
+    log(f"archive: {len(tensors)} tensors, {len(table)} blocks, {arc_off / 1e9:.3f} GB encoded, "
+        f"{out_off / 1e9:.3f} GB raw, built in {time.time() - t0:.0f}s")
+    return d_arc, table, meta, out_off, encs
+
+
+def verify(torch, d_out, meta) -> bool:
+    """Bit-exact check at full size: the decoded archive equals the regenerated inputs."""
+    ok = True
+    for name, shape, seed, off, nbytes in meta:
+        want = gen_bf16(torch, shape, seed, name.endswith("norm")).view(torch.uint8).reshape(-1)
+        if not torch.equal(d_out[off:off + nbytes], want):
+            log(f"MISMATCH in {name}")
+            ok = False
+    return ok
+
+
+def time_events(torch, fn, steps: int, stream) -> float:
+    """Milliseconds per call of fn() over `steps` calls, HIP events on `stream`."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def gemv_bench(torch, lib, rows: int, cols: int, copies: int, steps: int, warmup: int, stream) -> dict:
+    """Fused batch-1 decode-GEMV over `copies` resident copies of one parallel32 layer."""
+    import xksv_hip
+    w = gen_bf16(torch, (rows, cols), 77 + rows, False)
+    words = w.view(torch.int16).cpu().numpy().view(np.uint16)
+    enc, table = lib.encode_tensor(words, 2)
+    table = table.copy()
+    table["out_offset"] //= cols * 2  # GEMM plans index output rows
+    arcs = [torch.from_numpy(enc).to("cuda") for _ in range(copies)]
+    plan = xksv_hip.Plan(lib, table, enc.nbytes)
+    x = torch.randn(cols, device="cuda", dtype=torch.float32)
+    y = torch.empty(rows, device="cuda", dtype=torch.float32)
+    s = stream.cuda_stream
+    it = [0]
+
+    def step():
+        plan.gemm(arcs[it[0] % copies].data_ptr(), x.data_ptr(), 1, y.data_ptr(), s)
+        it[0] += 1
+
+    for _ in range(max(warmup, 1) * copies):
+        step()
+    nbad = plan.errors(s)[0]
+    ref = (w.double() @ x.double())
+    rel = (torch.linalg.norm(y.double() - ref) / torch.linalg.norm(ref)).item()
+    ms = time_events(torch, step, steps * copies, stream)
+    plan.close()
+    alg = enc.nbytes + cols * 4 + rows * 4
+    return {"us_per_layer": round(ms * 1e3, 2), "encoded_bytes": int(enc.nbytes),
+            "algorithmic_bytes": int(alg), "gbps": round(alg / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "rel_l2_vs_fp64": rel,
+            "errors": int(nbad), "copies": copies}
+
+
+def copy_bench(torch, steps: int, stream) -> float:
+    n = 1 << 31
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty(n, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    ms = time_events(torch, lambda: b.copy_(a), steps, stream)
+    return 2 * n / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(encs, table, max_slabs: int) -> dict | None:
+    """The reference's CPU decode (oracle/_ref, built from the reference's codec sources) on a
+    bounded sample of this archive's parallel32 blocks, one block per task on a thread pool."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_lib import REF_SO, Oracle, Reference
+    kind = "reference" if REF_SO.exists() else "port"
+    codec = Reference() if kind == "reference" else Oracle()
+    arc = np.concatenate(encs)
+    comp = table[table["codec"] == 2]
+    step = max(1, len(comp) // max_slabs)
+    sample = comp[::step][:max_slabs]
+    blobs = [arc[t["offset"]:t["offset"] + t["size"]].tobytes() for t in sample]
+    raw = int(sample["raw_size"].sum())
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+
+    def one(b):
+        rc, out = codec.unpack_parallel(b)
+        return rc
+
+    t0 = time.time()
+    with ThreadPoolExecutor(cores) as ex:
+        rcs = list(ex.map(one, blobs))
+    dt = time.time() - t0
+    if any(rcs):
+        return None
+    return {"value": round(raw / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": f"{len(blobs)} parallel32 blocks spread over the archive, {raw / 1e6:.0f} MB decoded, "
+                      f"{dt:.1f}s wall on {cores} threads"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=32, help="decoder layers in the archive (headline: 32)")
+    ap.add_argument("--gemv-copies", type=int, default=16)
+    ap.add_argument("--cpu-slabs", type=int, default=6000)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the compressed-weight path is built and measured on a single "
+              "MI355X (multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
+        return 2
+    import torch
+    import xksv_hip
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    lib = xksv_hip.Library()
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+
+    d_arc, table, meta, raw_total, encs = build_archive(torch, lib, args.layers, 2)
+    d_out = torch.empty(raw_total, dtype=torch.uint8, device="cuda")
+    plan = xksv_hip.Plan(lib, table, d_arc.numel())
+    step = lambda: plan.decode(d_arc.data_ptr(), d_out.data_ptr(), raw_total, s)  # noqa: E731
+    for _ in range(args.warmup):
+        step()
+    nbad, first, bits = plan.errors(s)
+    verified = nbad == 0 and verify(torch, d_out, meta)
+    log(f"decode errors={nbad} verified={verified}")
+    ms = time_events(torch, step, args.steps, stream)
+    nbad2 = plan.errors(s)[0]
+    decoded_gbps = raw_total / (ms * 1e-3) / 1e9
+    alg_bytes = int(d_arc.numel()) + raw_total
+    achieved = alg_bytes / (ms * 1e-3) / 1e9
+    log(f"decode {ms:.3f} ms/step, {decoded_gbps:.1f} GB/s decoded, {achieved:.1f} GB/s algorithmic")
+
+    g1 = gemv_bench(torch, lib, 14336, 4096, args.gemv_copies, args.steps, args.warmup, stream)
+    g2 = gemv_bench(torch, lib, 4096, 14336, args.gemv_copies, args.steps, args.warmup, stream)
+    log(f"gemv 14336x4096 {g1['us_per_layer']} us, 4096x14336 {g2['us_per_layer']} us")
+    copy_gbps = copy_bench(torch, 10, stream)
+
+    traffic = None
+    tpath = ROOT / "profiles" / "decode_llama3_8b_traffic.json"
+    if tpath.exists():
+        try:
+            traffic = json.loads(tpath.read_text()).get("traffic_bytes_per_launch")
+        except Exception:
+            traffic = None
+    cpu = None if args.no_cpu_baseline else cpu_baseline(encs, table, args.cpu_slabs)
+
+    line = {
+        "metric": METRIC, "value": round(decoded_gbps, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+        "config": {"workload": "llama3-8b-shaped archive, dfloat11-parallel (XKSP2 parallel32), whole-archive decode",
+                   "layers": args.layers, "blocks": int(len(table)), "elements": raw_total // 2,
+                   "encoded_bytes": int(d_arc.numel()), "decoded_bytes": raw_total,
+                   "compressed_ratio": round(d_arc.numel() / raw_total, 4), "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+        "bit_exact_full_size": bool(verified and nbad2 == 0),
+        "hbm_pct_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
+        "gemv_us_per_layer_14336x4096": g1["us_per_layer"],
+        "gemv_14336x4096": g1, "gemv_4096x14336": g2,
+        "hbm_copy_gbps": round(copy_gbps, 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -34,7 +34,8 @@ namespace {
 
 constexpr uint32_t kWave = 64;
 constexpr uint32_t kChunk = 96;                     // code bits per lane per segment
-constexpr uint32_t kRegion = kChunk + 4;            // lane scratch stride: 25 dwords, odd -> conflict-free
+constexpr uint32_t kSlack = 8;                      // bytes in front of a lane's speculative symbols
+constexpr uint32_t kRegion = kSlack + kChunk + 4;   // lane scratch stride: 27 dwords, odd -> conflict-free
 constexpr uint32_t kSegBits = kWave * kChunk;       // 6144 bits per segment
 constexpr uint32_t kCarry = 256;                    // room for an unconsumed partial tile
 constexpr uint32_t kSymsBytes = kCarry + kWave * kRegion;
@@ -86,23 +87,52 @@ __device__ __forceinline__ uint32_t rdlane(uint32_t v, uint32_t l) { return __bu
 __device__ __forceinline__ uint64_t rdlane64(uint64_t v, uint32_t l) {
   return (uint64_t)rdlane((uint32_t)v, l) | ((uint64_t)rdlane((uint32_t)(v >> 32), l) << 32);
 }
-template <typename T>
-__device__ __forceinline__ T wave_incl(T v, uint32_t lane) {
-#pragma unroll
-  for (uint32_t d = 1; d < kWave; d <<= 1) {
-    T o = __shfl_up(v, d, kWave);
-    if (lane >= d) v += o;
-  }
+// Wave64 scans and reductions with DPP row shifts and row broadcasts
+// (6 DPP operations per 32-bit scan).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return __builtin_amdgcn_update_dpp(0u, v, CTRL, ROW_MASK, 0xf, true);
+}
+__device__ __forceinline__ uint32_t wave_incl(uint32_t v, uint32_t) {
+  v += dpp<0x111>(v);
+  v += dpp<0x112>(v);
+  v += dpp<0x114>(v);
+  v += dpp<0x118>(v);
+  v += dpp<0x142, 0xa>(v);
+  v += dpp<0x143, 0xc>(v);
   return v;
 }
-template <typename T>
-__device__ __forceinline__ T wave_max(T v) {
-#pragma unroll
-  for (uint32_t d = kWave / 2; d >= 1; d >>= 1) {
-    T o = __shfl_xor(v, d, kWave);
-    v = v > o ? v : o;
+__device__ __forceinline__ uint64_t wave_incl(uint64_t v, uint32_t) {
+#define XKSV_STEP64(C, RM)                                                               \
+  {                                                                                      \
+    const uint32_t lo = dpp<C, RM>((uint32_t)v), hi = dpp<C, RM>((uint32_t)(v >> 32)); \
+    v += ((uint64_t)hi << 32) | lo;                                                      \
   }
+  XKSV_STEP64(0x111, 0xf) XKSV_STEP64(0x112, 0xf) XKSV_STEP64(0x114, 0xf) XKSV_STEP64(0x118, 0xf)
+  XKSV_STEP64(0x142, 0xa) XKSV_STEP64(0x143, 0xc)
+#undef XKSV_STEP64
   return v;
+}
+// Maximum over the wave (unsigned), broadcast to every lane.
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
+  v = max(v, dpp<0x111>(v));
+  v = max(v, dpp<0x112>(v));
+  v = max(v, dpp<0x114>(v));
+  v = max(v, dpp<0x118>(v));
+  v = max(v, dpp<0x142, 0xa>(v));
+  v = max(v, dpp<0x143, 0xc>(v));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+// Value of lane - 1 (0 for lane 0).
+__device__ __forceinline__ uint32_t from_prev_lane(uint32_t v) { return dpp<0x138>(v); }
+// Orders this wave's LDS accesses across lanes: LDS executes a wave's
+// operations in issue order, so a compiler fence is all a wave needs.  The
+// per-stream engine synchronises only within its wave (several waves of one
+// workgroup run independent streams and reach different numbers of these).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 __device__ __forceinline__ uint64_t ldg64(const uint8_t* p) {
   uint64_t v;
@@ -158,15 +188,22 @@ __device__ __forceinline__ float bf_lo(uint32_t pair) { return __uint_as_float(p
 __device__ __forceinline__ float bf_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
 
 // Tiled position q of a rows x cols slab -> (row, col)          [src/layout.cpp:36-48]
-__device__ __forceinline__ void tile_to_rc(uint64_t q, uint64_t rows, uint64_t cols, uint64_t& row, uint64_t& col) {
-  const uint64_t band = q / (16 * cols);
-  const uint64_t nr = (rows - 16 * band) < 16 ? (rows - 16 * band) : 16;
-  const uint64_t local = q - band * 16 * cols;
-  const uint64_t t = local / (nr * 16);
-  const uint64_t lt = local - t * nr * 16;
-  const uint64_t width = (cols - 16 * t) < 16 ? (cols - 16 * t) : 16;
-  row = 16 * band + lt / width;
-  col = 16 * t + lt % width;
+// 32-bit arithmetic: rows * cols < 2^31 on the device path.
+__device__ __forceinline__ void tile_to_rc(uint32_t q, uint32_t rows, uint32_t cols, uint32_t& row, uint32_t& col) {
+  uint32_t band = 0, local = q, nr = rows;
+  if (rows > 16) {  // 16 * cols <= rows * cols here
+    const uint32_t bsz = 16u * cols;
+    band = q / bsz;
+    local = q - band * bsz;
+    nr = min(16u, rows - 16u * band);
+  }
+  const uint32_t tsz = nr * 16u;
+  const uint32_t t = local / tsz;
+  const uint32_t lt = local - t * tsz;
+  const uint32_t width = min(16u, cols - 16u * t);
+  const uint32_t r = width == 16 ? (lt >> 4) : lt / width;
+  row = 16u * band + r;
+  col = 16u * t + (lt - r * width);
 }
 
 // ---------------------------------------------------------- block headers
@@ -179,58 +216,6 @@ struct Stream {
   uint32_t count;          // elements in this stream
   uint32_t start;          // tiled position of the stream's first element in its slab
 };
-
-// XKSP2 header and substream k                                   [src/c_api.cpp:66-85]
-// Returns error bits; `chunks` is set (> 0) once the block-level checks pass.
-__device__ uint32_t parse_parallel(const uint8_t* blk, uint64_t size, const DevBlock& d, uint32_t k,
-                                   uint32_t lane, Stream& st, uint32_t& chunks) {
-  chunks = 0;
-  if (size < 32) return kErrHeader;
-  const uint64_t hv = lane < 4 ? ldg64(blk + 8 * lane) : 0;
-  const uint64_t magic = rdlane64(hv, 0), rows = rdlane64(hv, 1), cols = rdlane64(hv, 2), nch = rdlane64(hv, 3);
-  if (magic != kMagicXKSP2 || !rows || rows > 16 || !cols || !nch || nch > 32 || cols > ~0ull / rows)
-    return kErrHeader;
-  const uint64_t total = rows * cols;
-  if (nch > total || total > size || total > ~0ull / 32 || size < 32 + 8 * nch) return kErrHeader;
-  if (rows != d.rows || cols != d.cols || total > kMaxBlockElems) return kErrShape;
-  const uint64_t len = lane < nch ? ldg64(blk + 32 + 8 * lane) : 0;
-  if (__ballot(lane < nch && (len < 272 || len > size))) return kErrHeader;
-  const uint64_t incl = wave_incl(len, lane);
-  const uint64_t hdr = 32 + 8 * nch;
-  if (hdr + rdlane64(incl, (uint32_t)nch - 1) != size) return kErrHeader;
-  chunks = (uint32_t)nch;
-  if (k >= chunks) return 0;
-  const uint64_t slen = rdlane64(len, k);
-  const uint64_t off = hdr + rdlane64(incl, k) - slen;
-  const uint64_t fv = lane < 2 ? ldg64(blk + off + 8 * lane) : 0;
-  const uint64_t cnt = rdlane64(fv, 0), nb = rdlane64(fv, 1);
-  const uint64_t s0 = total * k / nch, s1 = total * (k + 1) / nch;
-  if (cnt != s1 - s0 || cnt > slen - 272 || nb / 8 + (nb % 8 != 0) != slen - 272 - cnt) return kErrHeader;
-  st.lengths = blk + off + 16;
-  st.sm = blk + off + 272;
-  st.bits = st.sm + cnt;
-  st.nbits = nb;
-  st.count = (uint32_t)cnt;
-  st.start = (uint32_t)s0;
-  return 0;
-}
-
-// Serial block: [u64 count][u64 bits][256 lengths][count sm][codes] [src/c_api.cpp:29-34, cuda/decode.cu:49-51]
-__device__ uint32_t parse_serial(const uint8_t* blk, uint64_t size, const DevBlock& d, uint32_t lane, Stream& st) {
-  const uint64_t rows = d.rows, cols = d.cols;
-  if (size < 272 || !rows || !cols || cols > ~0ull / rows) return kErrHeader;
-  const uint64_t fv = lane < 2 ? ldg64(blk + 8 * lane) : 0;
-  const uint64_t cnt = rdlane64(fv, 0), nb = rdlane64(fv, 1);
-  if (cnt != rows * cols || cnt > size - 272 || nb / 8 + (nb % 8 != 0) != size - 272 - cnt) return kErrHeader;
-  if (cnt > kMaxBlockElems) return kErrShape;
-  st.lengths = blk + 16;
-  st.sm = blk + 272;
-  st.bits = st.sm + cnt;
-  st.nbits = nb;
-  st.count = (uint32_t)cnt;
-  st.start = 0;
-  return 0;
-}
 
 // ------------------------------------------------------------ code tables
 
@@ -264,19 +249,19 @@ __device__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uin
     const uint32_t t = s0 + lane;
     const bool valid = t < m;
     if (lane < 40) F.slots[lane] = 0;
-    __syncthreads();
+    wave_sync();
     const uint32_t ent = valid ? compact[t] : 0u;
     const uint32_t l = ent >> 8;
     if (valid) atomicOr(reinterpret_cast<unsigned long long*>(&F.slots[l]), 1ull << lane);
-    __syncthreads();
+    wave_sync();
     const uint64_t mk = valid ? F.slots[l] : 0ull;
     const uint32_t rin = mbcnt(mk);
     const uint32_t r = valid ? rin + F.cnt[l] : 0u;
-    __syncthreads();
+    wave_sync();
     if (valid && rin == 0) F.cnt[l] += (uint32_t)__popcll(mk);
     if (valid) rank[t] = (uint8_t)r;
   }
-  __syncthreads();
+  wave_sync();
   // Per-length group sums: C(l+1) = sum_{l' <= l} cnt[l'] * 2^(32 - l').
   const uint32_t c = (lane >= 1 && lane <= 32) ? F.cnt[lane] : 0u;
   const uint64_t g = (lane >= 1 && lane <= 32) ? ((uint64_t)c << (32 - lane)) : 0ull;
@@ -289,20 +274,23 @@ __device__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uin
   }
   if (lane < 16) F.l4[lane] = 0;
   if (total > (1ull << 32)) return Book{kErrCodebook, maxlen, true};
-  __syncthreads();
+  wave_sync();
   for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
     const uint32_t t = s0 + lane;
     if (t < m) {
       const uint32_t ent = compact[t], l = ent >> 8, sym = ent & 255u, r = rank[t];
       const uint64_t code = F.lim[l - 1] + ((uint64_t)r << (32 - l));
       S.sorted[F.base[l] + r] = (uint8_t)sym;
-      if (l <= 4) {
-        const uint32_t e0 = (uint32_t)(code >> 28), n = 1u << (4 - l);
-        for (uint32_t i = 0; i < n; ++i) F.l4[e0 + i] = (uint16_t)((l << 8) | sym);
+      if (l <= 4) {  // 2^(4-l) entries, naturally aligned
+        const uint32_t e0 = (uint32_t)(code >> 28), v = (l << 8) | sym, v2 = v | (v << 16);
+        if (l == 1) *reinterpret_cast<uint4*>(&F.l4[e0]) = make_uint4(v2, v2, v2, v2);
+        else if (l == 2) *reinterpret_cast<uint2*>(&F.l4[e0]) = make_uint2(v2, v2);
+        else if (l == 3) *reinterpret_cast<uint32_t*>(&F.l4[e0]) = v2;
+        else F.l4[e0] = (uint16_t)v;
       }
     }
   }
-  __syncthreads();
+  wave_sync();
   {  // codes of <= 4 bits cover whole 64-entry blocks of the 10-bit LUT
     const uint32_t e4 = F.l4[lane >> 2];
     const uint32_t pair = e4 | (e4 << 16);
@@ -310,37 +298,52 @@ __device__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uin
     *reinterpret_cast<uint4*>(&F.lut[16 * lane]) = v;
     *reinterpret_cast<uint4*>(&F.lut[16 * lane + 8]) = v;
   }
-  __syncthreads();
+  wave_sync();
   for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
     const uint32_t t = s0 + lane;
     if (t < m) {
       const uint32_t ent = compact[t], l = ent >> 8, sym = ent & 255u, r = rank[t];
-      if (l >= 5 && l <= kLutBits) {
+      if (l >= 5 && l <= kLutBits) {  // 2^(10-l) entries, naturally aligned
         const uint64_t code = F.lim[l - 1] + ((uint64_t)r << (32 - l));
-        const uint32_t e0 = (uint32_t)(code >> (32 - kLutBits)), n = 1u << (kLutBits - l);
-        for (uint32_t i = 0; i < n; ++i) F.lut[e0 + i] = (uint16_t)((l << 8) | sym);
+        const uint32_t e0 = (uint32_t)(code >> (32 - kLutBits)), v = (l << 8) | sym, v2 = v | (v << 16);
+        const uint4 v8 = make_uint4(v2, v2, v2, v2);
+        if (l <= 7) {
+          uint4* q = reinterpret_cast<uint4*>(&F.lut[e0]);
+          q[0] = v8;
+          if (l <= 6) q[1] = v8;
+          if (l == 5) {
+            q[2] = v8;
+            q[3] = v8;
+          }
+        } else if (l == 8) {
+          *reinterpret_cast<uint2*>(&F.lut[e0]) = make_uint2(v2, v2);
+        } else if (l == 9) {
+          *reinterpret_cast<uint32_t*>(&F.lut[e0]) = v2;
+        } else {
+          F.lut[e0] = (uint16_t)v;
+        }
       }
     }
   }
-  __syncthreads();
+  wave_sync();
   return Book{0, maxlen, true};
 }
 
 // Tables for codes longer than 32 bits (bit-serial path).  cnt/base/sorted
 // as above; open[l] counts length-l prefixes that longer codes extend, so a
 // prefix beyond them is an invalid code [src/codec.cpp:69 "invalid bitstream"].
-__device__ Book build_slow(Smem& S, uint32_t lane, const uint8_t* lengths, uint32_t maxlen) {
+__device__ Book build_slow(Smem& S, uint32_t lane, uint32_t lw, uint32_t maxlen) {
   SlowTables& T = S.t.s;
   uint8_t* lens = S.syms + 1024;
-  reinterpret_cast<uint32_t*>(lens)[lane] = ldg32(lengths + 4 * lane);
+  reinterpret_cast<uint32_t*>(lens)[lane] = lw;
   for (uint32_t i = lane; i < 256; i += kWave) T.cnt[i] = 0;
-  __syncthreads();
+  wave_sync();
 #pragma unroll
   for (uint32_t q = 0; q < 4; ++q) {
     const uint32_t l = lens[4 * lane + q];
     if (l) atomicAdd(&T.cnt[l], 1u);
   }
-  __syncthreads();
+  wave_sync();
   if (lane == 0) {
     uint32_t err = 0, free = 2, b = 0;
     for (uint32_t l = 1; l < 256; ++l) {
@@ -363,16 +366,16 @@ __device__ Book build_slow(Smem& S, uint32_t lane, const uint8_t* lengths, uint3
     }
     S.bcast[0] = err;
   }
-  __syncthreads();
+  wave_sync();
   return Book{S.bcast[0], maxlen, false};
 }
 
-__device__ Book build_book(Smem& S, uint32_t lane, const uint8_t* lengths) {
-  const uint32_t lw = ldg32(lengths + 4 * lane);
+// `lw` holds the code lengths of symbols 4 lane .. 4 lane + 3.
+__device__ Book build_book(Smem& S, uint32_t lane, uint32_t lw) {
   const uint32_t L0 = lw & 255u, L1 = (lw >> 8) & 255u, L2 = (lw >> 16) & 255u, L3 = lw >> 24;
   const uint32_t mx = max(max(L0, L1), max(L2, L3));
   const uint32_t maxlen = wave_max(mx);
-  if (maxlen > kMaxLenFast) return build_slow(S, lane, lengths, maxlen);
+  if (maxlen > kMaxLenFast) return build_slow(S, lane, lw, maxlen);
   return build_fast(S, lane, L0, L1, L2, L3, maxlen);
 }
 
@@ -389,99 +392,210 @@ __device__ __forceinline__ uint32_t long_code(const Smem& S, uint32_t w, uint32_
   return (l << 8) | S.sorted[idx];
 }
 
-// Decode codewords starting in [from, ce) (bits relative to the segment).
-// Symbols go to the lane's scratch region; `mask` records codeword starts
-// within [cs, cs + 32); `dead` marks a window that matches no code.
-__device__ __forceinline__ void run_chunk(const Smem& S, uint32_t from, uint32_t cs, uint32_t ce, uint8_t* region,
-                                          uint32_t maxlen, uint32_t& cnt, uint32_t& ex, uint32_t& mask,
-                                          uint32_t& dead) {
-  uint32_t p = from, c = 0, m = 0, d = 0;
-  while (p < ce) {
-    const uint32_t i = (p + 31) >> 5;
-    const uint32_t w = __builtin_amdgcn_alignbit(S.stream[i], S.stream[i + 1], 0u - p);
-    uint32_t e = S.t.f.lut[w >> (32 - kLutBits)];
+// A lane's decoded path through its chunk: codewords start at `start` and
+// run until `ex` (the first start at or past the chunk end); the `cnt`
+// symbols sit at region[base ...]; `mask` marks the path's starts within
+// [cs, cs + 32); `dead` = a window matched no code.
+struct Path {
+  uint32_t start, base, cnt, ex, mask, dead;
+};
+
+// One codeword at bit p from the register window (w0, w1, w2 = segment
+// dwords (p+31)/32 - 1 .. +1).  Returns (len << 8) | symbol, 0 if invalid,
+// and slides the window when the codeword crosses a dword boundary; the
+// third dword is re-read from LDS off the dependency chain.
+__device__ __forceinline__ uint32_t step(const Smem& S, uint32_t& p, uint32_t& w0, uint32_t& w1, uint32_t& w2,
+                                         uint32_t maxlen) {
+  const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
+  uint32_t e = S.t.f.lut[win >> (32 - kLutBits)];
+  if (e == 0) e = long_code(S, win, maxlen);
+  const uint32_t i0 = (p + 31) >> 5;
+  p += e >> 8;
+  const uint32_t i1 = (p + 31) >> 5;
+  const bool adv = i1 != i0;
+  w0 = adv ? w1 : w0;
+  w1 = adv ? w2 : w1;
+  w2 = S.stream[i1 + 2];
+  return e;
+}
+
+__device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
+  const uint32_t i = (p + 31) >> 5;
+  w0 = S.stream[i];
+  w1 = S.stream[i + 1];
+  w2 = S.stream[i + 2];
+}
+
+// Decode codewords starting in [from, ce) into region[base ...].
+__device__ __forceinline__ void decode_path(const Smem& S, uint32_t from, uint32_t cs, uint32_t ce, uint8_t* region,
+                                            uint32_t base, uint32_t maxlen, Path& P) {
+  uint32_t p = from, c = 0, m = 0, d = 0, w0, w1, w2;
+  load_window(S, p, w0, w1, w2);
+  uint8_t* out = region + base;
+  while (p < ce && p - cs < 32) {  // starts inside the synchronisation window
+    const uint32_t at = p;
+    const uint32_t e = step(S, p, w0, w1, w2, maxlen);
     if (e == 0) {
-      e = long_code(S, w, maxlen);
+      p = at;
+      d = 1;
+      break;
+    }
+    m |= 1u << (at - cs);
+    out[c++] = (uint8_t)e;
+  }
+  if (!d)
+    while (p < ce) {
+      const uint32_t at = p;
+      const uint32_t e = step(S, p, w0, w1, w2, maxlen);
       if (e == 0) {
+        p = at;
         d = 1;
         break;
       }
+      out[c++] = (uint8_t)e;
     }
+  P.start = from;
+  P.base = base;
+  P.cnt = c;
+  P.ex = p;
+  P.mask = m;
+  P.dead = d;
+}
+
+// The true entry pe is not on the lane's speculative path: decode from pe
+// until the true path reaches one of the recorded starts (the paths agree
+// from there on), keep the speculative tail and splice the new codewords in
+// front of it using the slack bytes.  False when no merge happens within
+// the window or the slack (the caller then re-decodes the whole chunk).
+__device__ __forceinline__ bool merge_path(const Smem& S, uint32_t pe, uint32_t cs, uint32_t ce, uint8_t* region,
+                                           uint32_t maxlen, Path& P) {
+  if (P.base != kSlack || P.start != cs) return false;
+  uint32_t p = pe, k = 0, m = 0, w0, w1, w2;
+  load_window(S, p, w0, w1, w2);
+  for (;;) {
     const uint32_t rel = p - cs;
-    if (rel < 32) m |= 1u << rel;
-    region[c++] = (uint8_t)e;
-    p += e >> 8;
+    if (rel >= 32 || p >= ce || k >= kSlack) return false;
+    if ((P.mask >> rel) & 1u) break;
+    const uint32_t e = step(S, p, w0, w1, w2, maxlen);
+    if (e == 0) return false;
+    m |= 1u << rel;
+    region[k++] = (uint8_t)e;
   }
-  cnt = c;
-  ex = p;
-  mask = m;
-  dead = d;
+  const uint32_t rel = p - cs, below = (1u << rel) - 1u;
+  const uint32_t j = (uint32_t)__popc(P.mask & below);
+  const uint32_t dst = kSlack + j - k;
+  for (uint32_t q = k; q-- > 0;) region[dst + q] = region[q];
+  P.base = dst;
+  P.cnt = P.cnt - j + k;
+  P.start = pe;
+  P.mask = m | (P.mask & ~below);
+  return true;
+}
+
+// Inputs of a stream's first segment, loaded ahead of use: the stream
+// header words (lanes 0, 1), the 256 code lengths (4 per lane) and the first
+// 784 code bytes (16 per lane, lanes < kStreamLanes).
+struct StreamIn {
+  uint64_t hdr;
+  uint32_t lens;
+  uint4 bits;
+};
+// Sign/mantissa bytes of the first 256 units (2048 positions) a consume call
+// will see: unit lane + 64 i in v[i].
+struct SmWin {
+  uint64_t v[4];
+};
+
+// `seg` .. `seg_end` is one serial block or XKSP2 segment; `count` is the
+// element count the block header implies (checked against the stream header
+// when the loads are used).  All loads stay inside [seg, seg_end).
+__device__ __forceinline__ void issue_stream(StreamIn& P, const uint8_t* seg, const uint8_t* seg_end, uint32_t count,
+                                             uint32_t lane) {
+  P.hdr = lane < 2 ? ldg64(seg + 8 * lane) : 0ull;
+  P.lens = ldg32(seg + 16 + 4 * lane);
+  P.bits = lane < kStreamLanes ? ldg16_bounded(seg + 272 + (uint64_t)count + 16 * lane, seg_end)
+                               : make_uint4(0u, 0u, 0u, 0u);
+}
+__device__ __forceinline__ void issue_sm(SmWin& W, const uint8_t* sm, uint32_t pos0, uint32_t count, uint32_t lane) {
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) {
+    const uint32_t p = pos0 + 8 * (lane + kWave * i);
+    W.v[i] = p + 8 <= count ? ldg64(sm + p) : 0ull;
+  }
+}
+__device__ __forceinline__ void stage_bits(Smem& S, uint32_t lane, uint4 v) {
+  if (lane < kStreamLanes) {
+    uint32_t* w = &S.stream[1 + 4 * lane];
+    w[0] = bswap32(v.x);
+    w[1] = bswap32(v.y);
+    w[2] = bswap32(v.z);
+    w[3] = bswap32(v.w);
+  }
 }
 
 // Decode one stream with the fast tables; the consumer receives the
-// exponents in stream order.  Returns error bits.
+// exponents in stream order.  `first` holds the stream's first 784 code
+// bytes; later segments are loaded one segment ahead.  Returns error bits.
 template <class Cons>
 __device__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen, const uint8_t* blk_end,
-                                Cons& C) {
+                                const uint4 first, Cons& C) {
   const uint64_t nbits = st.nbits;
   const uint8_t* bend = st.bits + ((nbits + 7) >> 3);
   if (bend > blk_end) bend = blk_end;
   uint8_t* const region = S.syms + kCarry + lane * kRegion;
   uint32_t carry = 0, pos0 = 0, entry = 0, err = 0;
   uint64_t S0 = 0, true_pos = 0;
+  uint4 cur = first;
   if (lane == 0) S.stream[0] = 0;
   while (true_pos < nbits) {
-    if (lane < kStreamLanes) {
-      const uint4 v = ldg16_bounded(st.bits + (S0 >> 3) + 16 * lane, bend);
-      uint32_t* w = &S.stream[1 + 4 * lane];
-      w[0] = bswap32(v.x);
-      w[1] = bswap32(v.y);
-      w[2] = bswap32(v.z);
-      w[3] = bswap32(v.w);
-    }
-    __syncthreads();
+    stage_bits(S, lane, cur);
+    wave_sync();
+    // Next segment's code bytes and this segment's sign/mantissa window go
+    // out now and land while the segment decodes.
+    if (S0 + kSegBits < nbits && lane < kStreamLanes)
+      cur = ldg16_bounded(st.bits + ((S0 + kSegBits) >> 3) + 16 * lane, bend);
+    SmWin W;
+    issue_sm(W, st.sm, pos0, st.count, lane);
     const uint64_t left = nbits - S0;
     const uint32_t lim_bits = left < kSegBits ? (uint32_t)left : kSegBits;
     const uint32_t cs = lane * kChunk;
     const bool active = cs < lim_bits;
     const uint32_t ce = active ? min(cs + kChunk, lim_bits) : cs;
-    uint32_t start = cs, cnt = 0, ex = cs, mask = 0, dead = 0;
-    if (active) run_chunk(S, cs, cs, ce, region, maxlen, cnt, ex, mask, dead);
+    Path P{cs, kSlack, 0, cs, 0, 0};
+    if (active) decode_path(S, cs, cs, ce, region, kSlack, maxlen, P);
     // Resolve: lane i is consistent when its predecessor's exit is a
     // codeword start on lane i's path.  Lanes before the first
     // inconsistent lane are on the true path.
     for (;;) {
-      uint32_t pe = __shfl_up(ex, 1, kWave), pd = __shfl_up(dead, 1, kWave);
+      uint32_t pe = from_prev_lane(P.ex), pd = from_prev_lane(P.dead);
       if (lane == 0) {
         pe = entry;
         pd = 0;
       }
       const uint32_t off = pe - cs;
-      const bool ok = !active || (!pd && (pe == start || (off < 32 && ((mask >> off) & 1u))));
+      const bool ok = !active || (!pd && (pe == P.start || (off < 32 && ((P.mask >> off) & 1u))));
       const uint64_t bad = __ballot(!ok);
-      const uint64_t deadm = __ballot(active && dead);
+      const uint64_t deadm = __ballot(active && P.dead);
       const uint64_t resolved = bad ? ((1ull << (__ffsll((unsigned long long)bad) - 1)) - 1) : ~0ull;
       if (deadm & resolved) {
         err = kErrStream;
         break;
       }
       if (!bad) break;
-      if (!ok && !pd) {
-        start = pe;
-        run_chunk(S, pe, cs, ce, region, maxlen, cnt, ex, mask, dead);
-      }
+      if (!ok && !pd && !merge_path(S, pe, cs, ce, region, maxlen, P)) decode_path(S, pe, cs, ce, region, 0, maxlen, P);
     }
     if (err) break;
-    uint32_t pe = __shfl_up(ex, 1, kWave);
+    uint32_t pe = from_prev_lane(P.ex);
     if (lane == 0) pe = entry;
     const uint32_t off = pe - cs;
-    const uint32_t skip = (active && off < 32) ? (uint32_t)__popc(mask & ((1u << off) - 1u)) : 0u;
-    const uint32_t t = active ? cnt - skip : 0u;
+    const uint32_t j = (!active || pe == P.start) ? 0u : (uint32_t)__popc(P.mask & ((1u << off) - 1u));
+    const uint32_t first = P.base + j;
+    const uint32_t t = active ? P.cnt - j : 0u;
     const uint32_t tinc = wave_incl(t, lane);
     const uint32_t total = rdlane(tinc, kWave - 1);
     const uint64_t act = __ballot(active);
     const uint32_t last = 63u - (uint32_t)__clzll((long long)act);
-    const uint32_t seg_exit = rdlane(ex, last);
+    const uint32_t seg_exit = rdlane(P.ex, last);
     if ((uint64_t)pos0 + carry + total > st.count) {
       err = kErrStream;  // more codewords than elements: trailing bits
       break;
@@ -495,9 +609,9 @@ __device__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32
 #pragma unroll
       for (uint32_t q = 0; q < kChunk / 4; ++q) {
         if (q >= ndmax) break;
-        R[q] = q < nd ? lds32(region + skip + 4 * q) : 0u;
+        R[q] = q < nd ? lds32(region + first + 4 * q) : 0u;
       }
-      __syncthreads();
+      wave_sync();
 #pragma unroll
       for (uint32_t q = 0; q < kChunk / 4; ++q) {
         if (q >= ndmax) break;
@@ -510,27 +624,26 @@ __device__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32
           if (tail > 2) p[2] = (uint8_t)(R[q] >> 16);
         }
       }
-      __syncthreads();
+      wave_sync();
     }
     const uint32_t avail = carry + total;
-    const uint32_t take = C.consume(S, lane, st, pos0, avail, false);
+    const bool fin = S0 + seg_exit >= nbits;  // last segment: hand over everything
+    const uint32_t take = C.consume(S, lane, st, pos0, avail, fin, W);
     const uint32_t rem = avail - take;
     if (take && rem) {  // take is a multiple of 256 here, so source and destination do not overlap
       const uint32_t v = 4 * lane < rem ? lds32(S.syms + take + 4 * lane) : 0u;
-      __syncthreads();
+      wave_sync();
       if (4 * lane < rem) sts32(S.syms + 4 * lane, v);
     }
-    __syncthreads();
+    wave_sync();
     carry = rem;
     pos0 += take;
     true_pos = S0 + seg_exit;
     entry = seg_exit - kSegBits;
     S0 += kSegBits;
   }
-  if (!err) {
-    if (true_pos != nbits || (uint64_t)pos0 + carry != st.count) err = kErrStream;
-    else if (carry) C.consume(S, lane, st, pos0, carry, true);
-  }
+  if (!err && (true_pos != nbits || (uint64_t)pos0 + carry != st.count)) err = kErrStream;
+  wave_sync();
   return err;
 }
 
@@ -548,7 +661,10 @@ __device__ uint32_t decode_slow(Smem& S, uint32_t lane, const Stream& st, Cons& 
     if (lane == 0) {
       uint32_t e = 0;
       for (uint32_t i = 0; i < nseg && !e; ++i) {
-        if (pos >= nbits) { e = kErrStream; break; }
+        if (pos >= nbits) {
+          e = kErrStream;
+          break;
+        }
         uint32_t d = (st.bits[pos >> 3] >> (7 - (pos & 7))) & 1u;
         ++pos;
         for (uint32_t l = 1;; ++l) {
@@ -557,33 +673,54 @@ __device__ uint32_t decode_slow(Smem& S, uint32_t lane, const Stream& st, Cons& 
             break;
           }
           d -= T.cnt[l];
-          if (d >= T.open[l] || l >= 255 || pos >= nbits) { e = kErrStream; break; }
+          if (d >= T.open[l] || l >= 255 || pos >= nbits) {
+            e = kErrStream;
+            break;
+          }
           d = 2 * d + ((st.bits[pos >> 3] >> (7 - (pos & 7))) & 1u);
           ++pos;
         }
       }
       S.bcast[0] = e;
     }
-    __syncthreads();
+    wave_sync();
     err = S.bcast[0];
-    __syncthreads();
+    wave_sync();
     if (err) break;
-    C.consume(S, lane, st, produced, nseg, produced + nseg == st.count);
-    __syncthreads();
+    SmWin W;
+    issue_sm(W, st.sm, produced, st.count, lane);
+    C.consume(S, lane, st, produced, nseg, produced + nseg == st.count, W);
+    wave_sync();
     produced += nseg;
   }
   if (lane == 0) S.bcast[1] = (pos == nbits);
-  __syncthreads();
+  wave_sync();
   if (!err && !S.bcast[1]) err = kErrStream;
-  __syncthreads();
+  wave_sync();
   return err;
 }
 
+// One stream from prefetched inputs P.  Before any work, the next stream's
+// inputs are issued into PN (when `nseg` is given) so they load while this
+// stream decodes.
 template <class Cons>
-__device__ uint32_t decode_stream(Smem& S, uint32_t lane, const Stream& st, const uint8_t* blk_end, Cons& C) {
-  const Book b = build_book(S, lane, st.lengths);
+__device__ uint32_t run_stream(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end, uint32_t count,
+                               uint32_t start, const StreamIn& P, Cons& C, const uint8_t* nseg,
+                               const uint8_t* nseg_end, uint32_t ncount, StreamIn& PN) {
+  if (nseg) issue_stream(PN, nseg, nseg_end, ncount, lane);
+  const uint64_t len = (uint64_t)(seg_end - seg);
+  const uint64_t cnt = rdlane64(P.hdr, 0), nb = rdlane64(P.hdr, 1);
+  if (cnt != count || cnt > len - 272 || nb / 8 + (nb % 8 != 0) != len - 272 - cnt) return kErrHeader;
+  Stream st;
+  st.lengths = seg + 16;
+  st.sm = seg + 272;
+  st.bits = st.sm + cnt;
+  st.nbits = nb;
+  st.count = count;
+  st.start = start;
+  const Book b = build_book(S, lane, P.lens);
   if (b.err) return b.err;
-  return b.fast ? decode_fast(S, lane, st, b.maxlen, blk_end, C) : decode_slow(S, lane, st, C);
+  return b.fast ? decode_fast(S, lane, st, b.maxlen, seg_end, P.bits, C) : decode_slow(S, lane, st, C);
 }
 
 // ------------------------------------------------------------- consumers
@@ -591,54 +728,56 @@ __device__ uint32_t decode_stream(Smem& S, uint32_t lane, const Stream& st, cons
 // Unit = 8 consecutive tiled positions = half a tile row.  A stream is
 // "unit-aligned" when its slab has full 16x16 tiles and the stream starts and
 // ends on unit boundaries; then unit u holds row (u/2)%16, columns 16*(u/32)+8*(u%2).
-__device__ __forceinline__ bool unit_aligned(const Stream& st, uint64_t rows, uint64_t cols) {
-  return rows % 16 == 0 && cols % 16 == 0 && st.start % 8 == 0 && st.count % 8 == 0;
+__device__ __forceinline__ bool unit_aligned(uint32_t start, uint32_t count, uint64_t rows, uint64_t cols) {
+  return rows % 16 == 0 && cols % 16 == 0 && start % 8 == 0 && count % 8 == 0;
 }
 
-// BF16 writer, unit-aligned streams: 16-byte stores of whole half tile rows.
-struct WriterAligned {
+// BF16 writer: 16-byte stores of half tile rows for unit-aligned streams,
+// one element per lane per step otherwise.
+struct Writer {
   uint8_t* out;  // slab base
-  uint32_t cols, tpb;
-  __device__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final) {
+  uint64_t rows, cols;
+  uint32_t tpb;  // tiles per 16-row band
+  bool aligned;
+  __device__ __forceinline__ void unit(const Smem& S, const Stream& st, uint32_t pos0, uint32_t u, uint64_t M) const {
+    uint64_t E;
+    __builtin_memcpy(&E, S.syms + 8 * u, 8);
+    const uint4 w = combine8(E, M);
+    const uint32_t U = ((st.start + pos0) >> 3) + u, T = U >> 5;
+    const uint32_t band = rows == 16 ? 0u : T / tpb;
+    const uint32_t row = 16u * band + ((U >> 1) & 15u);
+    const uint32_t col = 16u * (T - band * tpb) + 8u * (U & 1u);
+    __builtin_memcpy(out + 2ull * (row * (uint32_t)cols + col), &w, 16);
+  }
+  __device__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final,
+                              const SmWin& W) {
+    if (!aligned) {
+      for (uint32_t i = lane; i < avail; i += kWave) {
+        const uint32_t P = pos0 + i;
+        const uint32_t e = S.syms[i], s = st.sm[P];
+        const uint16_t w = (uint16_t)(((s & 0x80u) << 8) | (e << 7) | (s & 0x7fu));
+        uint32_t row, col;
+        tile_to_rc(st.start + P, (uint32_t)rows, (uint32_t)cols, row, col);
+        __builtin_memcpy(out + 2ull * (row * (uint32_t)cols + col), &w, 2);
+      }
+      return avail;
+    }
     const uint32_t take = final ? avail : (avail & ~255u);
     const uint32_t units = take >> 3;
-    const uint32_t U0 = (st.start + pos0) >> 3;
-    for (uint32_t u = lane; u < units; u += kWave) {
-      uint64_t E;
-      __builtin_memcpy(&E, S.syms + 8 * u, 8);
-      const uint64_t M = ldg64(st.sm + pos0 + 8 * u);
-      const uint4 w = combine8(E, M);
-      const uint32_t U = U0 + u, T = U >> 5;
-      const uint32_t band = T / tpb;
-      const uint64_t row = 16ull * band + ((U >> 1) & 15u);
-      const uint64_t col = 16ull * (T - band * tpb) + 8u * (U & 1u);
-      __builtin_memcpy(out + (row * cols + col) * 2, &w, 16);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint32_t u = lane + kWave * i;
+      if (u < units) unit(S, st, pos0, u, W.v[i]);
     }
+    for (uint32_t u = lane + 4 * kWave; u < units; u += kWave) unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
     return take;
   }
 };
 
-// BF16 writer, any shape: one element per lane per step.
-struct WriterGeneric {
-  uint8_t* out;
-  uint64_t rows, cols;
-  __device__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool) {
-    for (uint32_t i = lane; i < avail; i += kWave) {
-      const uint32_t P = pos0 + i;
-      const uint32_t e = S.syms[i], s = st.sm[P];
-      const uint16_t w = (uint16_t)(((s & 0x80u) << 8) | (e << 7) | (s & 0x7fu));
-      uint64_t row, col;
-      tile_to_rc((uint64_t)st.start + P, rows, cols, row, col);
-      __builtin_memcpy(out + (row * cols + col) * 2, &w, 2);
-    }
-    return avail;
-  }
-};
-
-// Fused GEMM/GEMV over one unit-aligned stream of a 16-row slab, fp32
-// activations X[c * ldx + j] (cuda/decode.cu:94 layout, batch columns
-// j < nb).  Every lane keeps one row: unit u = lane + 64 i has row
-// ((U0 + u) / 2) % 16, which does not depend on i.
+// Fused GEMM over unit-aligned streams of 16-row slabs, fp32 activations
+// X[c * ldx + j] (cuda/decode.cu:94 layout, batch columns j < nb).  Lane
+// `lane` accumulates unit u = lane + 64 i of every consume call; its row is
+// ((start / 8 + lane) / 2) % 16 for the whole stream.
 template <int NB>
 struct GemmF32 {
   const float* x;
@@ -649,40 +788,48 @@ struct GemmF32 {
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = 0.f;
   }
-  __device__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final) {
-    const uint32_t take = final ? avail : (avail & ~255u);
-    const uint32_t units = take >> 3;
-    const uint32_t U0 = (st.start + pos0) >> 3;
-    for (uint32_t u = lane; u < units; u += kWave) {
-      uint64_t E;
-      __builtin_memcpy(&E, S.syms + 8 * u, 8);
-      const uint64_t M = ldg64(st.sm + pos0 + 8 * u);
-      const uint4 w = combine8(E, M);
-      const uint32_t U = U0 + u;
-      const uint64_t col = 16ull * (U >> 5) + 8u * (U & 1u);
-      float f[8] = {bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y), bf_lo(w.z), bf_hi(w.z), bf_lo(w.w), bf_hi(w.w)};
-      if (NB == 1) {
-        float4 xa, xb;
-        __builtin_memcpy(&xa, x + col, 16);
-        __builtin_memcpy(&xb, x + col + 4, 16);
-        acc[0] = fmaf(f[0], xa.x, acc[0]);
-        acc[0] = fmaf(f[1], xa.y, acc[0]);
-        acc[0] = fmaf(f[2], xa.z, acc[0]);
-        acc[0] = fmaf(f[3], xa.w, acc[0]);
-        acc[0] = fmaf(f[4], xb.x, acc[0]);
-        acc[0] = fmaf(f[5], xb.y, acc[0]);
-        acc[0] = fmaf(f[6], xb.z, acc[0]);
-        acc[0] = fmaf(f[7], xb.w, acc[0]);
-      } else {
+  __device__ __forceinline__ void unit(const Smem& S, const Stream& st, uint32_t pos0, uint32_t u, uint64_t M) {
+    uint64_t E;
+    __builtin_memcpy(&E, S.syms + 8 * u, 8);
+    const uint4 w = combine8(E, M);
+    const uint32_t U = ((st.start + pos0) >> 3) + u;
+    const uint64_t col = 16ull * (U >> 5) + 8u * (U & 1u);
+    const float f[8] = {bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y),
+                        bf_lo(w.z), bf_hi(w.z), bf_lo(w.w), bf_hi(w.w)};
+    if (NB == 1) {
+      float4 xa, xb;
+      __builtin_memcpy(&xa, x + col, 16);
+      __builtin_memcpy(&xb, x + col + 4, 16);
+      float a = acc[0];
+      a = fmaf(f[0], xa.x, a);
+      a = fmaf(f[1], xa.y, a);
+      a = fmaf(f[2], xa.z, a);
+      a = fmaf(f[3], xa.w, a);
+      a = fmaf(f[4], xb.x, a);
+      a = fmaf(f[5], xb.y, a);
+      a = fmaf(f[6], xb.z, a);
+      a = fmaf(f[7], xb.w, a);
+      acc[0] = a;
+    } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float* xr = x + (col + i) * ldx;
+      for (int i = 0; i < 8; ++i) {
+        const float* xr = x + (col + i) * ldx;
 #pragma unroll
-          for (int j = 0; j < NB; ++j)
-            if (j < (int)nb) acc[j] = fmaf(f[i], xr[j], acc[j]);
-        }
+        for (int j = 0; j < NB; ++j)
+          if (j < (int)nb) acc[j] = fmaf(f[i], xr[j], acc[j]);
       }
     }
+  }
+  __device__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final,
+                              const SmWin& W) {
+    const uint32_t take = final ? avail : (avail & ~255u);
+    const uint32_t units = take >> 3;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint32_t u = lane + kWave * i;
+      if (u < units) unit(S, st, pos0, u, W.v[i]);
+    }
+    for (uint32_t u = lane + 4 * kWave; u < units; u += kWave) unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
     return take;
   }
   // Four lanes share each row: with s = (stream start / 8) % 2, lane l and
@@ -704,101 +851,201 @@ __device__ __forceinline__ void set_status(uint32_t* status, uint32_t slot, uint
   if (err && lane == 0) atomicOr(status + slot, err);
 }
 
-// Decode a list of blocks of one codec into BF16.  Task = (block, substream)
-// for parallel blocks, = block for serial blocks.
-__global__ void __launch_bounds__(64) k_decode(const DevBlock* __restrict__ blocks, uint32_t nblocks, uint32_t codec,
-                                               const uint8_t* __restrict__ arc, uint8_t* __restrict__ out,
-                                               uint32_t* __restrict__ status) {
+// Up to 36 leading 64-bit words of a block (XKSP2 header + segment lengths),
+// one per lane, never reading past the block.
+__device__ __forceinline__ uint64_t issue_head(const uint8_t* blk, uint64_t size, uint32_t lane) {
+  if (lane >= 36) return 0ull;
+  const uint64_t at = 8ull * lane;
+  if (at + 8 <= size) return ldg64(blk + at);
+  uint64_t v = 0;
+  for (uint64_t i = 0; i < 8; ++i)
+    if (at + i < size) v |= (uint64_t)blk[at + i] << (8 * i);
+  return v;
+}
+
+// XKSP2 block header checks [src/c_api.cpp:66-72, 78, cuda/parallel.cu:132-139]
+// on the words from issue_head.  Sets chunks; lane 4 + k holds segment k's length.
+__device__ __forceinline__ uint32_t check_head(uint64_t hv, uint64_t size, const DevBlock& d, uint32_t lane,
+                                               uint32_t& chunks) {
+  chunks = 0;
+  if (size < 32) return kErrHeader;
+  const uint64_t magic = rdlane64(hv, 0), rows = rdlane64(hv, 1), cols = rdlane64(hv, 2), nch = rdlane64(hv, 3);
+  if (magic != kMagicXKSP2 || !rows || rows > 16 || !cols || !nch || nch > 32 || cols > ~0ull / rows)
+    return kErrHeader;
+  const uint64_t total = rows * cols;
+  if (nch > total || total > size || total > ~0ull / 32 || size < 32 + 8 * nch) return kErrHeader;
+  if (rows != d.rows || cols != d.cols || total > kMaxBlockElems) return kErrShape;
+  const bool mine = lane >= 4 && lane < 4 + nch;
+  const uint64_t len = mine ? hv : 0ull;
+  if (__ballot(mine && (len < 272 || len > size))) return kErrHeader;
+  const uint64_t sum = rdlane64(wave_incl(len, lane), 63);
+  if (32 + 8 * nch + sum != size) return kErrHeader;
+  chunks = (uint32_t)nch;
+  return 0;
+}
+
+// Decode XKSP2 blocks: one wave per block, its substreams in order, each
+// substream's inputs prefetched while the previous one decodes; the next
+// block's header is prefetched at the start of each block.
+__global__ void __launch_bounds__(64) k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+                                                        const uint8_t* __restrict__ arc, uint8_t* __restrict__ out,
+                                                        uint32_t* __restrict__ status) {
   __shared__ Smem S;
   const uint32_t lane = lane_id();
-  const uint32_t per = codec == kCodecParallel ? kMaxChunks : 1u;
-  const uint64_t ntasks = (uint64_t)nblocks * per;
-  for (uint64_t task = blockIdx.x; task < ntasks; task += gridDim.x) {
-    const uint32_t b = (uint32_t)(task / per), k = (uint32_t)(task % per);
+  uint32_t b = blockIdx.x;
+  uint64_t hv = b < nblocks ? issue_head(arc + blocks[b].src, blocks[b].size, lane) : 0ull;
+  for (; b < nblocks; b += gridDim.x) {
     const DevBlock d = blocks[b];
     const uint8_t* blk = arc + d.src;
-    Stream st;
-    uint32_t err, chunks = 1;
-    if (codec == kCodecParallel) err = parse_parallel(blk, d.size, d, k, lane, st, chunks);
-    else err = parse_serial(blk, d.size, d, lane, st);
-    if (!err && k >= chunks) continue;
-    if (!err) {
-      if (unit_aligned(st, d.rows, d.cols)) {
-        WriterAligned C{out + d.dst, (uint32_t)d.cols, (uint32_t)(d.cols / 16)};
-        err = decode_stream(S, lane, st, blk + d.size, C);
-      } else {
-        WriterGeneric C{out + d.dst, d.rows, d.cols};
-        err = decode_stream(S, lane, st, blk + d.size, C);
-      }
+    uint32_t chunks;
+    uint32_t err = check_head(hv, d.size, d, lane, chunks);
+    const uint64_t seglen_v = hv;
+    const uint32_t bn = b + gridDim.x;
+    if (bn < nblocks) hv = issue_head(arc + blocks[bn].src, blocks[bn].size, lane);
+    if (err) {
+      set_status(status, d.status_slot, err, lane);
+      continue;
+    }
+    const uint64_t total = d.rows * d.cols;
+    const bool aligned = d.rows % 16 == 0 && d.cols % 16 == 0;
+    Writer C{out + d.dst, d.rows, d.cols, (uint32_t)(d.cols / 16), false};
+    uint64_t off = 32 + 8ull * chunks;
+    uint64_t len = rdlane64(seglen_v, 4);
+    StreamIn P, PN;
+    issue_stream(P, blk + off, blk + off + len, (uint32_t)(total / chunks), lane);
+    for (uint32_t k = 0; k < chunks && !err; ++k) {
+      const uint32_t s0 = (uint32_t)(total * k / chunks), s1 = (uint32_t)(total * (k + 1) / chunks);
+      const uint64_t noff = off + len;
+      const uint64_t nlen = k + 1 < chunks ? rdlane64(seglen_v, 4 + k + 1) : 0ull;
+      const uint32_t ncount = k + 1 < chunks ? (uint32_t)(total * (k + 2) / chunks) - s1 : 0u;
+      C.aligned = aligned && unit_aligned(s0, s1 - s0, d.rows, d.cols);
+      err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, P, C,
+                       k + 1 < chunks ? blk + noff : nullptr, blk + noff + nlen, ncount, PN);
+      P = PN;
+      off = noff;
+      len = nlen;
     }
     set_status(status, d.status_slot, err, lane);
-    __syncthreads();
+  }
+}
+
+// Decode serial blocks: one wave per block (one stream), the next block's
+// inputs prefetched while this one decodes.
+__global__ void __launch_bounds__(64) k_decode_serial(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+                                                      const uint8_t* __restrict__ arc, uint8_t* __restrict__ out,
+                                                      uint32_t* __restrict__ status) {
+  __shared__ Smem S;
+  const uint32_t lane = lane_id();
+  StreamIn P, PN;
+  uint32_t b = blockIdx.x;
+  if (b < nblocks && blocks[b].size >= 272)
+    issue_stream(P, arc + blocks[b].src, arc + blocks[b].src + blocks[b].size,
+                 (uint32_t)(blocks[b].rows * blocks[b].cols), lane);
+  for (; b < nblocks; b += gridDim.x) {
+    const DevBlock d = blocks[b];
+    const uint32_t bn = b + gridDim.x;
+    const bool has_next = bn < nblocks && blocks[bn].size >= 272;
+    const DevBlock dn = has_next ? blocks[bn] : d;
+    uint32_t err = 0;
+    if (d.size < 272 || !d.rows || !d.cols || d.cols > ~0ull / d.rows) err = kErrHeader;
+    else if (d.rows * d.cols > kMaxBlockElems) err = kErrShape;
+    if (!err) {
+      const uint32_t n = (uint32_t)(d.rows * d.cols);
+      Writer C{out + d.dst, d.rows, d.cols, (uint32_t)(d.cols / 16), unit_aligned(0, n, d.rows, d.cols)};
+      err = run_stream(S, lane, arc + d.src, arc + d.src + d.size, n, 0, P, C, has_next ? arc + dn.src : nullptr,
+                       arc + dn.src + dn.size, (uint32_t)(dn.rows * dn.cols), PN);
+    } else if (has_next) {
+      issue_stream(PN, arc + dn.src, arc + dn.src + dn.size, (uint32_t)(dn.rows * dn.cols), lane);
+    }
+    P = PN;
+    set_status(status, d.status_slot, err, lane);
   }
 }
 
 // Fused decode-GEMM for unit-aligned 16-row slabs, fp32 activations
-// X[c * ldx + j], output Y[(dst + r) * ldy + j].  Parallel blocks combine
-// their substreams' partial sums in substream order through `partial`
-// (kMaxChunks x 16 x NB floats per block) and a per-block arrival counter
-// that the last arriving wave resets, so the result is deterministic.
-template <int NB>
-__global__ void __launch_bounds__(64) k_gemm_f32(const DevBlock* __restrict__ blocks, uint32_t nblocks,
-                                                 uint32_t codec, const uint8_t* __restrict__ arc,
-                                                 const float* __restrict__ x, uint64_t ldx, uint32_t nb,
-                                                 float* __restrict__ y, uint64_t ldy, uint32_t* __restrict__ status,
-                                                 float* __restrict__ partial, uint32_t* __restrict__ counters) {
-  __shared__ Smem S;
-  const uint32_t lane = lane_id();
-  const uint32_t per = codec == kCodecParallel ? kMaxChunks : 1u;
-  const uint64_t ntasks = (uint64_t)nblocks * per;
-  for (uint64_t task = blockIdx.x; task < ntasks; task += gridDim.x) {
-    const uint32_t b = (uint32_t)(task / per), k = (uint32_t)(task % per);
+// X[c * ldx + j], output Y[(dst + r) * ldy + j].  One workgroup of W waves per
+// block: wave w takes substreams w, w + W, ... (prefetching each next one),
+// adds its per-row partial sums into its own LDS slots after every
+// substream, and the workgroup sums the W slots in wave order.  No atomics,
+// deterministic.
+template <int W, int NB>
+__global__ void __launch_bounds__(64 * W) k_gemm_f32(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+                                                     uint32_t codec, const uint8_t* __restrict__ arc,
+                                                     const float* __restrict__ x, uint64_t ldx, uint32_t nb,
+                                                     float* __restrict__ y, uint64_t ldy,
+                                                     uint32_t* __restrict__ status) {
+  __shared__ Smem SS[W];
+  __shared__ float red[W][16][NB];
+  __shared__ uint32_t werr[W];
+  const uint32_t lane = lane_id(), w = threadIdx.x / 64;
+  Smem& S = SS[w];
+  for (uint32_t b = blockIdx.x; b < nblocks; b += gridDim.x) {
     const DevBlock d = blocks[b];
     const uint8_t* blk = arc + d.src;
-    Stream st;
-    uint32_t err, chunks = 1;
-    if (codec == kCodecParallel) err = parse_parallel(blk, d.size, d, k, lane, st, chunks);
-    else err = parse_serial(blk, d.size, d, lane, st);
-    if (codec == kCodecParallel && chunks == 0) {  // block-level header failure: no reduction
-      set_status(status, d.status_slot, err, lane);
-      continue;
+    for (uint32_t i = lane; i < 16 * NB; i += kWave) red[w][i / NB][i % NB] = 0.f;
+    uint32_t err = 0, chunks = 1;
+    uint64_t hv = 0;
+    if (codec == kCodecParallel) {
+      hv = issue_head(blk, d.size, lane);
+      err = check_head(hv, d.size, d, lane, chunks);
+    } else if (d.size < 272 || d.rows != 16 || !d.cols || d.rows * d.cols > kMaxBlockElems) {
+      err = kErrHeader;
     }
-    if (k >= chunks) continue;
-    GemmF32<NB> C{x, ldx, nb};
-    C.init();
-    if (!err && (d.rows != 16 || !unit_aligned(st, d.rows, d.cols))) err = kErrShape;
-    if (!err) err = decode_stream(S, lane, st, blk + d.size, C);
-    const uint32_t su = (st.start >> 3) & 1u;
-    C.reduce(lane, su);
-    set_status(status, d.status_slot, err, lane);
-    // One holder lane per row: lanes < 32 with (lane + su) even hold slab row
-    // ((start / 8 + lane) / 2) % 16, sixteen distinct rows.
-    const uint32_t row = (((st.start >> 3) + lane) >> 1) & 15u;
-    const bool holder = lane < 32 && ((lane + su) & 1u) == 0;
-    if (codec != kCodecParallel) {
-      if (holder && !err)
+    if (!err && (d.rows != 16 || d.cols % 16)) err = kErrShape;
+    if (!err) {
+      const uint64_t total = d.rows * d.cols;
+      // segment offsets: walk to this wave's first substream
+      uint64_t off = codec == kCodecParallel ? 32 + 8ull * chunks : 0, len = d.size;
+      uint32_t k = w;
+      if (codec == kCodecParallel) {
+        for (uint32_t q = 0; q < k && q < chunks; ++q) off += rdlane64(hv, 4 + q);
+        len = k < chunks ? rdlane64(hv, 4 + k) : 0;
+      }
+      StreamIn P, PN;
+      if (k < chunks) issue_stream(P, blk + off, blk + off + len, (uint32_t)(total * (k + 1) / chunks - total * k / chunks), lane);
+      for (; k < chunks && !err; k += W) {
+        const uint32_t s0 = (uint32_t)(total * k / chunks), s1 = (uint32_t)(total * (k + 1) / chunks);
+        // next substream of this wave
+        uint64_t noff = off, nlen = 0;
+        const uint32_t kn = k + W;
+        if (kn < chunks) {
+          for (uint32_t q = k; q < kn; ++q) noff += rdlane64(hv, 4 + q);
+          nlen = rdlane64(hv, 4 + kn);
+        }
+        const uint32_t ncount = kn < chunks ? (uint32_t)(total * (kn + 1) / chunks - total * kn / chunks) : 0u;
+        if (!unit_aligned(s0, s1 - s0, d.rows, d.cols)) {
+          err = kErrShape;
+          break;
+        }
+        GemmF32<NB> C{x, ldx, nb, {}};
+        C.init();
+        err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, P, C, kn < chunks ? blk + noff : nullptr,
+                         blk + noff + nlen, ncount, PN);
+        const uint32_t su = (s0 >> 3) & 1u;
+        C.reduce(lane, su);
+        const uint32_t row = (((s0 >> 3) + lane) >> 1) & 15u;
+        if (lane < 32 && ((lane + su) & 1u) == 0)
 #pragma unroll
-        for (int j = 0; j < NB; ++j)
-          if (j < (int)nb) y[(d.dst + row) * ldy + j] = C.acc[j];
-    } else {
-      float* mine = partial + ((uint64_t)b * kMaxChunks + k) * 16 * NB;
-      if (holder)
-#pragma unroll
-        for (int j = 0; j < NB; ++j) mine[row * NB + j] = err ? 0.f : C.acc[j];
-      uint32_t old = 0;
-      if (lane == 0)
-        old = __hip_atomic_fetch_add(counters + b, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      old = rdlane(old, 0);
-      if (old == chunks - 1) {
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        for (uint32_t idx = lane; idx < 16u * NB; idx += kWave) {
-          const uint32_t r = idx / NB, j = idx % NB;
+          for (int j = 0; j < NB; ++j) red[w][row][j] += C.acc[j];
+        P = PN;
+        off = noff;
+        len = nlen;
+      }
+    }
+    if (lane == 0) werr[w] = err;
+    __syncthreads();
+    uint32_t any = 0;
+    for (uint32_t q = 0; q < W; ++q) any |= werr[q];
+    if (w == 0) {
+      set_status(status, d.status_slot, any, lane);
+      if (!any)
+        for (uint32_t i = lane; i < 16 * NB; i += kWave) {
+          const uint32_t r = i / NB, j = i % NB;
           float s = 0.f;
-          for (uint32_t q = 0; q < chunks; ++q) s += partial[(((uint64_t)b * kMaxChunks + q) * 16 + r) * NB + j];
+#pragma unroll
+          for (int q = 0; q < W; ++q) s += red[q][r][j];
           if (j < nb) y[(d.dst + r) * ldy + j] = s;
         }
-        if (lane == 0) __hip_atomic_store(counters + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
     }
     __syncthreads();
   }
@@ -839,10 +1086,10 @@ __global__ void __launch_bounds__(64) k_gemm_plain(const DevBlock* __restrict__ 
         for (uint64_t c = lane; c < d.cols; c += kWave) {
           uint16_t h;
           __builtin_memcpy(&h, wrow + 2 * c, 2);
-          const float w = __uint_as_float((uint32_t)h << 16);
+          const float wv = __uint_as_float((uint32_t)h << 16);
 #pragma unroll
           for (uint32_t j = 0; j < 4; ++j)
-            if (j0 + j < nb) a[j] = fmaf(w, x[c * ldx + j0 + j], a[j]);
+            if (j0 + j < nb) a[j] = fmaf(wv, x[c * ldx + j0 + j], a[j]);
         }
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
@@ -871,30 +1118,37 @@ static unsigned grid_for(uint64_t tasks, unsigned cap) {
 hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc, uint8_t* out,
                          uint32_t* status, unsigned max_groups, hipStream_t s) {
   if (!nblocks) return hipSuccess;
-  const uint64_t tasks = (uint64_t)nblocks * (codec == kCodecParallel ? kMaxChunks : 1u);
-  hipLaunchKernelGGL(k_decode, dim3(grid_for(tasks, max_groups)), dim3(64), 0, s, blocks, nblocks, codec, arc, out,
-                     status);
+  const dim3 g(grid_for(nblocks, max_groups)), blk(64);
+  if (codec == kCodecParallel)
+    hipLaunchKernelGGL(k_decode_parallel, g, blk, 0, s, blocks, nblocks, arc, out, status);
+  else
+    hipLaunchKernelGGL(k_decode_serial, g, blk, 0, s, blocks, nblocks, arc, out, status);
   return hipGetLastError();
+}
+
+template <int W>
+static void gemm_f32_w(dim3 g, hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec,
+                       const uint8_t* arc, const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy,
+                       uint32_t* status) {
+  const dim3 blk(64 * W);
+  if (nb == 1)
+    hipLaunchKernelGGL((k_gemm_f32<W, 1>), g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
+  else if (nb <= 4)
+    hipLaunchKernelGGL((k_gemm_f32<W, 4>), g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
+  else if (nb <= 8)
+    hipLaunchKernelGGL((k_gemm_f32<W, 8>), g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
+  else
+    hipLaunchKernelGGL((k_gemm_f32<W, 16>), g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
 }
 
 hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
-                           float* partial, uint32_t* counters, unsigned max_groups, hipStream_t s) {
+                           float*, uint32_t*, unsigned max_groups, hipStream_t s) {
   if (!nblocks) return hipSuccess;
-  const uint64_t tasks = (uint64_t)nblocks * (codec == kCodecParallel ? kMaxChunks : 1u);
-  const dim3 g(grid_for(tasks, max_groups)), blk(64);
-  if (nb == 1)
-    hipLaunchKernelGGL(k_gemm_f32<1>, g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, partial,
-                       counters);
-  else if (nb <= 4)
-    hipLaunchKernelGGL(k_gemm_f32<4>, g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, partial,
-                       counters);
-  else if (nb <= 8)
-    hipLaunchKernelGGL(k_gemm_f32<8>, g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, partial,
-                       counters);
+  if (codec == kCodecParallel)
+    gemm_f32_w<4>(dim3(grid_for(nblocks, max_groups / 4)), s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
   else
-    hipLaunchKernelGGL(k_gemm_f32<16>, g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status,
-                       partial, counters);
+    gemm_f32_w<1>(dim3(grid_for(nblocks, max_groups)), s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
   return hipGetLastError();
 }
 
