@@ -46,17 +46,28 @@ constexpr uint32_t kMaxLenFast = 32;
 constexpr uint32_t kSlowSeg = 4096;                 // symbols per bit-serial segment (multiple of 256)
 constexpr uint64_t kMagicXKSP2 = 0x0000003250534B58ull;  // "XKSP2\0\0\0" little-endian
 
+// Every function that takes the LDS block by reference is force-inlined: the
+// compiler then addresses it with DS instructions.  Through a call it would
+// become a generic pointer and FLAT instructions, which fault on LDS
+// addresses that are not naturally aligned (merged narrow stores can be).
+//
 // Per-wave LDS.  The table area is either the fast tables (LUT + per-length
 // limits) or the bit-serial tables; rank/compaction scratch lives in `syms`
 // before decoding starts.
+// Two-symbol lookup entry for a 10-bit window (0 = first code longer than 10
+// bits, or invalid):  bits 0-7 first symbol, 8-15 second symbol, 16-22 bits
+// consumed, 23 second symbol present, 24-27 length of the first code.
 struct FastTables {
-  uint16_t lut[1u << kLutBits];  // (len << 8) | symbol for codes of <= 10 bits; 0 = longer/invalid
+  uint32_t lut2[1u << kLutBits];
   uint64_t lim[40];              // lim[l] = left-aligned 32-bit end of the length-l codes, C(l+1)
   uint64_t slots[40];            // per-length lane masks (rank computation)
   uint32_t cnt[40];              // codes per length
   uint16_t base[40];             // index of the first length-l symbol in `sorted`
   uint16_t l4[16];               // codes of <= 4 bits, indexed by the top 4 bits
 };
+// The one-symbol table, (len << 8) | symbol, lives in the symbol buffer
+// while the tables are built.
+constexpr uint32_t kLut1Off = 1024;
 struct SlowTables {
   uint32_t cnt[256];
   uint16_t base[256];
@@ -231,7 +242,7 @@ struct Book {
 // C(l) = first code of length l; a symbol's code is C(l) + rank * 2^(32-l),
 // rank = number of smaller symbols of the same length.  The assignment is
 // oversubscribed (the reference throws) iff the Kraft total exceeds 2^32.
-__device__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uint32_t L2, uint32_t L3,
+__device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uint32_t L2, uint32_t L3,
                            uint32_t maxlen) {
   FastTables& F = S.t.f;
   uint16_t* compact = reinterpret_cast<uint16_t*>(S.syms);  // (len << 8) | symbol, symbol order
@@ -291,12 +302,13 @@ __device__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uin
     }
   }
   wave_sync();
+  uint16_t* lut1 = reinterpret_cast<uint16_t*>(S.syms + kLut1Off);
   {  // codes of <= 4 bits cover whole 64-entry blocks of the 10-bit LUT
     const uint32_t e4 = F.l4[lane >> 2];
     const uint32_t pair = e4 | (e4 << 16);
     const uint4 v = make_uint4(pair, pair, pair, pair);
-    *reinterpret_cast<uint4*>(&F.lut[16 * lane]) = v;
-    *reinterpret_cast<uint4*>(&F.lut[16 * lane + 8]) = v;
+    *reinterpret_cast<uint4*>(&lut1[16 * lane]) = v;
+    *reinterpret_cast<uint4*>(&lut1[16 * lane + 8]) = v;
   }
   wave_sync();
   for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
@@ -308,7 +320,7 @@ __device__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uin
         const uint32_t e0 = (uint32_t)(code >> (32 - kLutBits)), v = (l << 8) | sym, v2 = v | (v << 16);
         const uint4 v8 = make_uint4(v2, v2, v2, v2);
         if (l <= 7) {
-          uint4* q = reinterpret_cast<uint4*>(&F.lut[e0]);
+          uint4* q = reinterpret_cast<uint4*>(&lut1[e0]);
           q[0] = v8;
           if (l <= 6) q[1] = v8;
           if (l == 5) {
@@ -316,14 +328,35 @@ __device__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uin
             q[3] = v8;
           }
         } else if (l == 8) {
-          *reinterpret_cast<uint2*>(&F.lut[e0]) = make_uint2(v2, v2);
+          *reinterpret_cast<uint2*>(&lut1[e0]) = make_uint2(v2, v2);
         } else if (l == 9) {
-          *reinterpret_cast<uint32_t*>(&F.lut[e0]) = v2;
+          *reinterpret_cast<uint32_t*>(&lut1[e0]) = v2;
         } else {
-          F.lut[e0] = (uint16_t)v;
+          lut1[e0] = (uint16_t)v;
         }
       }
     }
+  }
+  wave_sync();
+  // Two-symbol table: entry e holds its first code and, when the code after
+  // it also ends within the 10-bit window, that one too.
+#pragma unroll
+  for (uint32_t g = 0; g < 4; ++g) {  // four entries at a time keeps register use low
+    const uint2 a = *reinterpret_cast<const uint2*>(&lut1[16 * lane + 4 * g]);
+    uint32_t o[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint32_t e = 16 * lane + 4 * g + i;
+      const uint32_t v = ((i < 2 ? a.x : a.y) >> (16 * (i & 1))) & 0xffffu;
+      const uint32_t l1 = v >> 8;
+      const uint32_t b = lut1[(e << l1) & ((1u << kLutBits) - 1)];
+      const uint32_t l2 = b >> 8;
+      const bool two = v != 0 && b != 0 && l1 + l2 <= kLutBits;
+      o[i] = v == 0 ? 0u
+                    : (v & 255u) | (two ? (b & 255u) << 8 : 0u) | ((two ? l1 + l2 : l1) << 16) | (two ? 1u << 23 : 0u) |
+                          (l1 << 24);
+    }
+    *reinterpret_cast<uint4*>(&F.lut2[16 * lane + 4 * g]) = make_uint4(o[0], o[1], o[2], o[3]);
   }
   wave_sync();
   return Book{0, maxlen, true};
@@ -332,7 +365,7 @@ __device__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uin
 // Tables for codes longer than 32 bits (bit-serial path).  cnt/base/sorted
 // as above; open[l] counts length-l prefixes that longer codes extend, so a
 // prefix beyond them is an invalid code [src/codec.cpp:69 "invalid bitstream"].
-__device__ Book build_slow(Smem& S, uint32_t lane, uint32_t lw, uint32_t maxlen) {
+__device__ __forceinline__ Book build_slow(Smem& S, uint32_t lane, uint32_t lw, uint32_t maxlen) {
   SlowTables& T = S.t.s;
   uint8_t* lens = S.syms + 1024;
   reinterpret_cast<uint32_t*>(lens)[lane] = lw;
@@ -371,7 +404,7 @@ __device__ Book build_slow(Smem& S, uint32_t lane, uint32_t lw, uint32_t maxlen)
 }
 
 // `lw` holds the code lengths of symbols 4 lane .. 4 lane + 3.
-__device__ Book build_book(Smem& S, uint32_t lane, uint32_t lw) {
+__device__ __forceinline__ Book build_book(Smem& S, uint32_t lane, uint32_t lw) {
   const uint32_t L0 = lw & 255u, L1 = (lw >> 8) & 255u, L2 = (lw >> 16) & 255u, L3 = lw >> 24;
   const uint32_t mx = max(max(L0, L1), max(L2, L3));
   const uint32_t maxlen = wave_max(mx);
@@ -400,22 +433,49 @@ struct Path {
   uint32_t start, base, cnt, ex, mask, dead;
 };
 
-// One codeword at bit p from the register window (w0, w1, w2 = segment
-// dwords (p+31)/32 - 1 .. +1).  Returns (len << 8) | symbol, 0 if invalid,
-// and slides the window when the codeword crosses a dword boundary; the
-// third dword is re-read from LDS off the dependency chain.
-__device__ __forceinline__ uint32_t step(const Smem& S, uint32_t& p, uint32_t& w0, uint32_t& w1, uint32_t& w2,
-                                         uint32_t maxlen) {
-  const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
-  uint32_t e = S.t.f.lut[win >> (32 - kLutBits)];
-  if (e == 0) e = long_code(S, win, maxlen);
-  const uint32_t i0 = (p + 31) >> 5;
-  p += e >> 8;
+// Slide the register window (w0, w1, w2 = segment dwords (p+31)/32 - 1 ..
+// +1) after p advanced from `from` by at most 32 bits; the third dword is
+// re-read from LDS off the dependency chain.
+__device__ __forceinline__ void slide(const Smem& S, uint32_t from, uint32_t p, uint32_t& w0, uint32_t& w1,
+                                      uint32_t& w2) {
   const uint32_t i1 = (p + 31) >> 5;
-  const bool adv = i1 != i0;
+  const bool adv = i1 != ((from + 31) >> 5);
   w0 = adv ? w1 : w0;
   w1 = adv ? w2 : w1;
   w2 = S.stream[i1 + 2];
+}
+
+// Up to two codewords at bit p (lut2 entry layout).  A window that matches no
+// code sets `dead` and moves p to ce, which ends the caller's loop.
+__device__ __forceinline__ uint32_t step2(const Smem& S, uint32_t& p, uint32_t ce, uint32_t& w0, uint32_t& w1,
+                                          uint32_t& w2, uint32_t maxlen, uint32_t& dead) {
+  const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
+  uint32_t e = S.t.f.lut2[win >> (32 - kLutBits)];
+  if (e == 0) {
+    const uint32_t lc = long_code(S, win, maxlen);
+    const uint32_t len = lc ? lc >> 8 : ce - p;
+    dead |= lc == 0;
+    e = (lc & 255u) | (len << 16) | (len << 24);
+  }
+  // A second codeword starting at or past ce belongs to the next chunk.
+  const uint32_t l1 = (e >> 24) & 15u;
+  if (((e >> 23) & 1u) && p + l1 >= ce) e = (e & 0x0f0000ffu) | (l1 << 16);
+  const uint32_t from = p;
+  p += (e >> 16) & 127u;
+  slide(S, from, p, w0, w1, w2);
+  return e;
+}
+
+// One codeword at bit p: (len << 8) | symbol, 0 if invalid.
+__device__ __forceinline__ uint32_t step1(const Smem& S, uint32_t& p, uint32_t& w0, uint32_t& w1, uint32_t& w2,
+                                          uint32_t maxlen) {
+  const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
+  const uint32_t e2 = S.t.f.lut2[win >> (32 - kLutBits)];
+  const uint32_t e = e2 ? (((e2 >> 24) & 15u) << 8) | (e2 & 255u) : long_code(S, win, maxlen);
+  if (e == 0) return 0;
+  const uint32_t from = p;
+  p += e >> 8;
+  slide(S, from, p, w0, w1, w2);
   return e;
 }
 
@@ -426,34 +486,29 @@ __device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t&
   w2 = S.stream[i + 2];
 }
 
-// Decode codewords starting in [from, ce) into region[base ...].
+// Decode codewords starting in [from, ce) into region[base ...], two per
+// lookup where the table allows.  Each store writes both symbol slots; the
+// count advances by the number present.
 __device__ __forceinline__ void decode_path(const Smem& S, uint32_t from, uint32_t cs, uint32_t ce, uint8_t* region,
                                             uint32_t base, uint32_t maxlen, Path& P) {
   uint32_t p = from, c = 0, m = 0, d = 0, w0, w1, w2;
   load_window(S, p, w0, w1, w2);
   uint8_t* out = region + base;
   while (p < ce && p - cs < 32) {  // starts inside the synchronisation window
-    const uint32_t at = p;
-    const uint32_t e = step(S, p, w0, w1, w2, maxlen);
-    if (e == 0) {
-      p = at;
-      d = 1;
-      break;
-    }
-    m |= 1u << (at - cs);
-    out[c++] = (uint8_t)e;
+    const uint32_t rel = p - cs;
+    const uint32_t e = step2(S, p, ce, w0, w1, w2, maxlen, d);
+    const uint32_t two = (e >> 23) & 1u, rel2 = rel + ((e >> 24) & 15u);
+    m |= (1u << rel) | (two && rel2 < 32 ? 1u << rel2 : 0u);
+    const uint16_t sy = (uint16_t)e;
+    __builtin_memcpy(out + c, &sy, 2);
+    c += 1 + two;
   }
-  if (!d)
-    while (p < ce) {
-      const uint32_t at = p;
-      const uint32_t e = step(S, p, w0, w1, w2, maxlen);
-      if (e == 0) {
-        p = at;
-        d = 1;
-        break;
-      }
-      out[c++] = (uint8_t)e;
-    }
+  while (p < ce) {
+    const uint32_t e = step2(S, p, ce, w0, w1, w2, maxlen, d);
+    const uint16_t sy = (uint16_t)e;
+    __builtin_memcpy(out + c, &sy, 2);
+    c += 1 + ((e >> 23) & 1u);
+  }
   P.start = from;
   P.base = base;
   P.cnt = c;
@@ -476,7 +531,7 @@ __device__ __forceinline__ bool merge_path(const Smem& S, uint32_t pe, uint32_t 
     const uint32_t rel = p - cs;
     if (rel >= 32 || p >= ce || k >= kSlack) return false;
     if ((P.mask >> rel) & 1u) break;
-    const uint32_t e = step(S, p, w0, w1, w2, maxlen);
+    const uint32_t e = step1(S, p, w0, w1, w2, maxlen);
     if (e == 0) return false;
     m |= 1u << rel;
     region[k++] = (uint8_t)e;
@@ -537,7 +592,7 @@ __device__ __forceinline__ void stage_bits(Smem& S, uint32_t lane, uint4 v) {
 // exponents in stream order.  `first` holds the stream's first 784 code
 // bytes; later segments are loaded one segment ahead.  Returns error bits.
 template <class Cons>
-__device__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen, const uint8_t* blk_end,
+__device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen, const uint8_t* blk_end,
                                 const uint4 first, Cons& C) {
   const uint64_t nbits = st.nbits;
   const uint8_t* bend = st.bits + ((nbits + 7) >> 3);
@@ -651,7 +706,7 @@ __device__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32
 // the code one bit at a time (d = offset from the first code of the current
 // length); the consumer sees the symbols kSlowSeg at a time.
 template <class Cons>
-__device__ uint32_t decode_slow(Smem& S, uint32_t lane, const Stream& st, Cons& C) {
+__device__ __forceinline__ uint32_t decode_slow(Smem& S, uint32_t lane, const Stream& st, Cons& C) {
   const SlowTables& T = S.t.s;
   const uint64_t nbits = st.nbits;
   uint64_t pos = 0;
@@ -704,7 +759,7 @@ __device__ uint32_t decode_slow(Smem& S, uint32_t lane, const Stream& st, Cons& 
 // inputs are issued into PN (when `nseg` is given) so they load while this
 // stream decodes.
 template <class Cons>
-__device__ uint32_t run_stream(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end, uint32_t count,
+__device__ __forceinline__ uint32_t run_stream(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end, uint32_t count,
                                uint32_t start, const StreamIn& P, Cons& C, const uint8_t* nseg,
                                const uint8_t* nseg_end, uint32_t ncount, StreamIn& PN) {
   if (nseg) issue_stream(PN, nseg, nseg_end, ncount, lane);
@@ -749,7 +804,7 @@ struct Writer {
     const uint32_t col = 16u * (T - band * tpb) + 8u * (U & 1u);
     __builtin_memcpy(out + 2ull * (row * (uint32_t)cols + col), &w, 16);
   }
-  __device__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final,
+  __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final,
                               const SmWin& W) {
     if (!aligned) {
       for (uint32_t i = lane; i < avail; i += kWave) {
@@ -784,7 +839,7 @@ struct GemmF32 {
   uint64_t ldx;
   uint32_t nb;
   float acc[NB];
-  __device__ void init() {
+  __device__ __forceinline__ void init() {
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = 0.f;
   }
@@ -820,7 +875,7 @@ struct GemmF32 {
       }
     }
   }
-  __device__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final,
+  __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final,
                               const SmWin& W) {
     const uint32_t take = final ? avail : (avail & ~255u);
     const uint32_t units = take >> 3;
@@ -835,7 +890,7 @@ struct GemmF32 {
   // Four lanes share each row: with s = (stream start / 8) % 2, lane l and
   // ((l + s) ^ 1) - s (mod 64) hold the two halves of a tile row, and l ^ 32
   // the same row two tiles on.  After the two exchanges all four hold the sum.
-  __device__ void reduce(uint32_t lane, uint32_t s) {
+  __device__ __forceinline__ void reduce(uint32_t lane, uint32_t s) {
     const int partner = (int)((((lane + s) ^ 1u) - s) & 63u);
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
@@ -887,7 +942,7 @@ __device__ __forceinline__ uint32_t check_head(uint64_t hv, uint64_t size, const
 // Decode XKSP2 blocks: one wave per block, its substreams in order, each
 // substream's inputs prefetched while the previous one decodes; the next
 // block's header is prefetched at the start of each block.
-__global__ void __launch_bounds__(64) k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
                                                         const uint8_t* __restrict__ arc, uint8_t* __restrict__ out,
                                                         uint32_t* __restrict__ status) {
   __shared__ Smem S;
@@ -931,7 +986,7 @@ __global__ void __launch_bounds__(64) k_decode_parallel(const DevBlock* __restri
 
 // Decode serial blocks: one wave per block (one stream), the next block's
 // inputs prefetched while this one decodes.
-__global__ void __launch_bounds__(64) k_decode_serial(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) k_decode_serial(const DevBlock* __restrict__ blocks, uint32_t nblocks,
                                                       const uint8_t* __restrict__ arc, uint8_t* __restrict__ out,
                                                       uint32_t* __restrict__ status) {
   __shared__ Smem S;
