@@ -23,6 +23,7 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 constexpr uint64_t kAlign = 256;
+constexpr uint64_t kQueues = 4;  // block-queue counters per plan (one per decode launch of a step)
 
 uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 uint64_t get64(const uint8_t* p) {
@@ -34,12 +35,11 @@ uint64_t get64(const uint8_t* p) {
 struct DeviceInfo {
   bool init = false, ok = false;
   int cus = 0;
-  unsigned max_groups = 0;
 };
 std::mutex g_dev_mu;
 DeviceInfo g_dev[kMaxDevices];
 
-// Current device and its persistent-grid size; nullptr without a device.
+// Current device and its CU count; nullptr without a device.
 const DeviceInfo* current_device(int* id_out) {
   int id = -1;
   if (hipGetDevice(&id) != hipSuccess || id < 0 || id >= kMaxDevices) return nullptr;
@@ -50,7 +50,6 @@ const DeviceInfo* current_device(int* id_out) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, id) == hipSuccess && cus > 0) {
       d.cus = cus;
-      d.max_groups = (unsigned)cus * 16u;
       d.ok = true;
     }
   }
@@ -130,7 +129,8 @@ int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows
     if (launch_fill_u32(status, (L.partial - L.status) / 4, 0, nullptr) != hipSuccess) break;
     const DevBlock* dd = reinterpret_cast<const DevBlock*>(b.p + L.desc);
     if (mode == 0) {
-      if (launch_decode(dd, 1, codec, b.p, static_cast<uint8_t*>(out), status, di->max_groups, nullptr) != hipSuccess)
+      if (launch_decode(dd, 1, codec, b.p, static_cast<uint8_t*>(out), status, nullptr, (unsigned)di->cus,
+                        nullptr) != hipSuccess)
         break;
     } else if (!generic_gemm) {
       bool ok = true;
@@ -138,12 +138,14 @@ int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows
         const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
         ok = launch_gemm_f32(dd, 1, codec, b.p, x + j0, batch, nb, static_cast<float*>(out) + j0, batch, status,
                              reinterpret_cast<float*>(b.p + L.partial),
-                             reinterpret_cast<uint32_t*>(b.p + L.counters), di->max_groups, nullptr) == hipSuccess;
+                             reinterpret_cast<uint32_t*>(b.p + L.counters), (unsigned)di->cus, nullptr) == hipSuccess;
       }
       if (!ok) break;
     } else {
       // Not unit-aligned: decode to scratch, then a plain deterministic GEMM.
-      if (launch_decode(dd, 1, codec, b.p, b.p + L.scratch, status, di->max_groups, nullptr) != hipSuccess) break;
+      if (launch_decode(dd, 1, codec, b.p, b.p + L.scratch, status, nullptr, (unsigned)di->cus, nullptr) !=
+          hipSuccess)
+        break;
       if (launch_gemm_plain(dd + 1, 1, b.p, x, batch, (uint32_t)batch, static_cast<float*>(out), batch, nullptr) !=
           hipSuccess)
         break;
@@ -442,8 +444,9 @@ int xksv_hip_plan_create(const xksv_hip_block* blocks, size_t nblocks, uint64_t 
   P->n_parallel = (uint32_t)par.size();
   P->n_raw = (uint32_t)raw.size();
   P->h_status.assign(nblocks ? nblocks : 1, 0);
-  ok = ok && hipMalloc(reinterpret_cast<void**>(&P->status), (nblocks ? nblocks : 1) * 4) == hipSuccess &&
-       launch_fill_u32(P->status, nblocks ? nblocks : 1, 0, nullptr) == hipSuccess &&
+  // Status words, then the decode launches' block queues (zeroed together).
+  ok = ok && hipMalloc(reinterpret_cast<void**>(&P->status), (nblocks + kQueues) * 4) == hipSuccess &&
+       launch_fill_u32(P->status, nblocks + kQueues, 0, nullptr) == hipSuccess &&
        hipStreamSynchronize(nullptr) == hipSuccess;
   if (!ok) {
     xksv_hip_plan_destroy(P);
@@ -474,10 +477,13 @@ int xksv_hip_plan_decode(xksv_hip_plan* P, const void* archive, void* out, uint6
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* arc = static_cast<const uint8_t*>(archive);
   uint8_t* o = static_cast<uint8_t*>(out);
-  if (launch_fill_u32(P->status, P->blocks.size(), 0, s) != hipSuccess) return 1;
-  if (launch_decode(P->d_parallel, P->n_parallel, kCodecParallel, arc, o, P->status, di->max_groups, s) != hipSuccess)
+  uint32_t* queue = P->status + P->blocks.size();
+  if (launch_fill_u32(P->status, P->blocks.size() + kQueues, 0, s) != hipSuccess) return 1;
+  if (launch_decode(P->d_parallel, P->n_parallel, kCodecParallel, arc, o, P->status, queue, (unsigned)di->cus, s) !=
+      hipSuccess)
     return 1;
-  if (launch_decode(P->d_serial, P->n_serial, kCodecSerial, arc, o, P->status, di->max_groups, s) != hipSuccess)
+  if (launch_decode(P->d_serial, P->n_serial, kCodecSerial, arc, o, P->status, queue + 1, (unsigned)di->cus, s) !=
+      hipSuccess)
     return 1;
   if (launch_copy_raw(P->d_raw, P->n_raw, arc, o, s) != hipSuccess) return 1;
   return 0;
@@ -490,19 +496,21 @@ int xksv_hip_plan_gemm(xksv_hip_plan* P, const void* archive, const float* x, si
   if (!di || !prepare_gemm(P)) return 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* arc = static_cast<const uint8_t*>(archive);
-  if (launch_fill_u32(P->status, P->blocks.size(), 0, s) != hipSuccess) return 1;
+  uint32_t* queue = P->status + P->blocks.size();
+  if (launch_fill_u32(P->status, P->blocks.size() + kQueues, 0, s) != hipSuccess) return 1;
   for (uint64_t j0 = 0; j0 < batch; j0 += kMaxFusedBatch) {
     const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
     if (launch_gemm_f32(P->g_fparallel, P->n_fparallel, kCodecParallel, arc, x + j0, batch, nb, y + j0, batch,
-                        P->status, P->partial, P->counters, di->max_groups, s) != hipSuccess)
+                        P->status, P->partial, P->counters, (unsigned)di->cus, s) != hipSuccess)
       return 1;
     if (launch_gemm_f32(P->g_fserial, P->n_fserial, kCodecSerial, arc, x + j0, batch, nb, y + j0, batch, P->status,
-                        P->partial, P->counters, di->max_groups, s) != hipSuccess)
+                        P->partial, P->counters, (unsigned)di->cus, s) != hipSuccess)
       return 1;
   }
-  if (launch_decode(P->g_gser, P->n_gser, kCodecSerial, arc, P->scratch, P->status, di->max_groups, s) !=
+  if (launch_decode(P->g_gser, P->n_gser, kCodecSerial, arc, P->scratch, P->status, queue + 2, (unsigned)di->cus, s) !=
           hipSuccess ||
-      launch_decode(P->g_gpar, P->n_gpar, kCodecParallel, arc, P->scratch, P->status, di->max_groups, s) != hipSuccess)
+      launch_decode(P->g_gpar, P->n_gpar, kCodecParallel, arc, P->scratch, P->status, queue + 3, (unsigned)di->cus,
+                    s) != hipSuccess)
     return 1;
   if (launch_gemm_plain(P->g_gplain, P->n_generic, P->scratch, x, batch, (uint32_t)batch, y, batch, s) != hipSuccess)
     return 1;

@@ -18,12 +18,14 @@ bool encode_serial(const uint8_t* data, uint64_t rows, uint64_t cols, std::vecto
 bool encode_parallel(const uint8_t* data, uint64_t rows, uint64_t cols, std::vector<uint8_t>& v);
 std::vector<SlabSpec> slab_rule(uint64_t nbytes, bool bf16, uint64_t shape_cols);
 
-// Kernel launchers (xksv_kernels.hip).  max_groups bounds the persistent grid.
+// Kernel launchers (xksv_kernels.hip).  `cus` = the device's CU count; each
+// launcher sizes its persistent grid to the workgroups resident at once.
+// `queue` (optional) is a zeroed counter the decode waves claim blocks from.
 hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc, uint8_t* out,
-                         uint32_t* status, unsigned max_groups, hipStream_t s);
+                         uint32_t* status, uint32_t* queue, unsigned cus, hipStream_t s);
 hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
-                           float* partial, uint32_t* counters, unsigned max_groups, hipStream_t s);
+                           float* partial, uint32_t* counters, unsigned cus, hipStream_t s);
 hipError_t launch_copy_raw(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint8_t* out, hipStream_t s);
 hipError_t launch_gemm_plain(const DevBlock* blocks, uint32_t nblocks, const uint8_t* base, const float* x,
                              uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, hipStream_t s);

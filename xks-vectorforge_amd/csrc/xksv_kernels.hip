@@ -939,23 +939,35 @@ __device__ __forceinline__ uint32_t check_head(uint64_t hv, uint64_t size, const
   return 0;
 }
 
+// The block this wave decodes after `b`.  With a queue (a counter the host
+// zeroes before the launch) the first gridDim.x blocks go one per workgroup and
+// each later one to whichever wave asks first, which balances blocks of
+// different sizes; without one, a grid stride.
+__device__ __forceinline__ uint32_t claim_next(uint32_t* queue, uint32_t b, uint32_t lane) {
+  if (!queue) return b + gridDim.x;
+  uint32_t t = 0;
+  if (lane == 0) t = atomicAdd(queue, 1u);
+  return gridDim.x + rdlane(t, 0);
+}
+
 // Decode XKSP2 blocks: one wave per block, its substreams in order, each
 // substream's inputs prefetched while the previous one decodes; the next
 // block's header is prefetched at the start of each block.
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
                                                         const uint8_t* __restrict__ arc, uint8_t* __restrict__ out,
-                                                        uint32_t* __restrict__ status) {
+                                                        uint32_t* __restrict__ status, uint32_t* queue) {
   __shared__ Smem S;
   const uint32_t lane = lane_id();
   uint32_t b = blockIdx.x;
   uint64_t hv = b < nblocks ? issue_head(arc + blocks[b].src, blocks[b].size, lane) : 0ull;
-  for (; b < nblocks; b += gridDim.x) {
+  for (uint32_t bn; b < nblocks; b = bn) {
     const DevBlock d = blocks[b];
     const uint8_t* blk = arc + d.src;
     uint32_t chunks;
     uint32_t err = check_head(hv, d.size, d, lane, chunks);
     const uint64_t seglen_v = hv;
-    const uint32_t bn = b + gridDim.x;
+    bn = claim_next(queue, b, lane);
     if (bn < nblocks) hv = issue_head(arc + blocks[bn].src, blocks[bn].size, lane);
     if (err) {
       set_status(status, d.status_slot, err, lane);
@@ -986,9 +998,9 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) k_
 
 // Decode serial blocks: one wave per block (one stream), the next block's
 // inputs prefetched while this one decodes.
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) k_decode_serial(const DevBlock* __restrict__ blocks, uint32_t nblocks,
-                                                      const uint8_t* __restrict__ arc, uint8_t* __restrict__ out,
-                                                      uint32_t* __restrict__ status) {
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+k_decode_serial(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_t* __restrict__ arc,
+                uint8_t* __restrict__ out, uint32_t* __restrict__ status, uint32_t* queue) {
   __shared__ Smem S;
   const uint32_t lane = lane_id();
   StreamIn P, PN;
@@ -996,9 +1008,9 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) k_
   if (b < nblocks && blocks[b].size >= 272)
     issue_stream(P, arc + blocks[b].src, arc + blocks[b].src + blocks[b].size,
                  (uint32_t)(blocks[b].rows * blocks[b].cols), lane);
-  for (; b < nblocks; b += gridDim.x) {
+  for (uint32_t bn; b < nblocks; b = bn) {
     const DevBlock d = blocks[b];
-    const uint32_t bn = b + gridDim.x;
+    bn = claim_next(queue, b, lane);
     const bool has_next = bn < nblocks && blocks[bn].size >= 272;
     const DevBlock dn = has_next ? blocks[bn] : d;
     uint32_t err = 0;
@@ -1170,40 +1182,59 @@ static unsigned grid_for(uint64_t tasks, unsigned cap) {
   return (unsigned)(tasks < cap ? (tasks ? tasks : 1) : cap);
 }
 
+// Workgroups of `kernel` resident at once on one CU; times the CU count this
+// is the persistent grid (a larger grid would run a second, partly idle round).
+template <class K>
+static unsigned groups_per_cu(K kernel, unsigned threads) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, (int)threads, 0) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  return (unsigned)per_cu;
+}
+
 hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc, uint8_t* out,
-                         uint32_t* status, unsigned max_groups, hipStream_t s) {
+                         uint32_t* status, uint32_t* queue, unsigned cus, hipStream_t s) {
   if (!nblocks) return hipSuccess;
-  const dim3 g(grid_for(nblocks, max_groups)), blk(64);
-  if (codec == kCodecParallel)
-    hipLaunchKernelGGL(k_decode_parallel, g, blk, 0, s, blocks, nblocks, arc, out, status);
-  else
-    hipLaunchKernelGGL(k_decode_serial, g, blk, 0, s, blocks, nblocks, arc, out, status);
+  const dim3 blk(64);
+  if (codec == kCodecParallel) {
+    static const unsigned per_cu = groups_per_cu(k_decode_parallel, 64);
+    hipLaunchKernelGGL(k_decode_parallel, dim3(grid_for(nblocks, per_cu * cus)), blk, 0, s, blocks, nblocks, arc, out,
+                       status, queue);
+  } else {
+    static const unsigned per_cu = groups_per_cu(k_decode_serial, 64);
+    hipLaunchKernelGGL(k_decode_serial, dim3(grid_for(nblocks, per_cu * cus)), blk, 0, s, blocks, nblocks, arc, out,
+                       status, queue);
+  }
   return hipGetLastError();
 }
 
+template <int W, int NB>
+static void gemm_f32_launch(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec,
+                            const uint8_t* arc, const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy,
+                            uint32_t* status, unsigned cus) {
+  static const unsigned per_cu = groups_per_cu(k_gemm_f32<W, NB>, 64 * W);
+  hipLaunchKernelGGL((k_gemm_f32<W, NB>), dim3(grid_for(nblocks, per_cu * cus)), dim3(64 * W), 0, s, blocks, nblocks, codec,
+                     arc, x, ldx, nb, y, ldy, status);
+}
+
 template <int W>
-static void gemm_f32_w(dim3 g, hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec,
-                       const uint8_t* arc, const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy,
-                       uint32_t* status) {
-  const dim3 blk(64 * W);
-  if (nb == 1)
-    hipLaunchKernelGGL((k_gemm_f32<W, 1>), g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
-  else if (nb <= 4)
-    hipLaunchKernelGGL((k_gemm_f32<W, 4>), g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
-  else if (nb <= 8)
-    hipLaunchKernelGGL((k_gemm_f32<W, 8>), g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
-  else
-    hipLaunchKernelGGL((k_gemm_f32<W, 16>), g, blk, 0, s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
+static void gemm_f32_w(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
+                       const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
+                       unsigned cus) {
+  if (nb == 1) gemm_f32_launch<W, 1>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
+  else if (nb <= 4) gemm_f32_launch<W, 4>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
+  else if (nb <= 8) gemm_f32_launch<W, 8>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
+  else gemm_f32_launch<W, 16>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
 }
 
 hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
-                           float*, uint32_t*, unsigned max_groups, hipStream_t s) {
+                           float*, uint32_t*, unsigned cus, hipStream_t s) {
   if (!nblocks) return hipSuccess;
   if (codec == kCodecParallel)
-    gemm_f32_w<4>(dim3(grid_for(nblocks, max_groups / 4)), s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
+    gemm_f32_w<4>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
   else
-    gemm_f32_w<1>(dim3(grid_for(nblocks, max_groups)), s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status);
+    gemm_f32_w<1>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
   return hipGetLastError();
 }
 
