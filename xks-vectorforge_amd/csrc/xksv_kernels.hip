@@ -14,13 +14,14 @@
 // stream at a time: a parallel32 substream, or a whole serial slab.  The
 // wave builds the stream's canonical-code lookup tables in LDS, stages the
 // code stream in LDS in segments of 64 x 96 bits, and every lane decodes one
-// 96-bit chunk speculatively from the chunk's first bit, recording which bit
-// positions of the chunk's first 32 bits start a codeword.  Codes are at most
-// 32 bits on this path, so the true entry into a chunk lies within those 32
-// bits; a lane is synchronised when its true entry is one of its recorded
-// starts, otherwise it re-decodes from the true entry.  A wave prefix sum
-// places each lane's symbols; the run is compacted in LDS and handed to a
-// consumer (BF16 writer, fused GEMV, fused GEMM) a whole 16x16 tile at a time.
+// 96-bit chunk.  Lane 0 starts at the segment's true entry; every other lane
+// starts decoding kSync bits before its chunk and drops what precedes the
+// chunk: Huffman codes resynchronise within a few codewords, so the lane's
+// first codeword start inside its chunk almost always equals the previous
+// lane's exit, which proves the lane is on the true path; a lane where it
+// does not re-decodes from that exit.  A wave prefix sum places each lane's
+// symbols; the run is compacted in LDS and handed to a consumer (BF16 writer,
+// fused GEMV, fused GEMM) a whole 16x16 tile at a time.
 // Streams with codes longer than 32 bits take a bit-serial path in the same
 // kernel.  Error semantics equal the reference's: a block fails iff the
 // reference's unpack fails on it.
@@ -34,8 +35,8 @@ namespace {
 
 constexpr uint32_t kWave = 64;
 constexpr uint32_t kChunk = 96;                     // code bits per lane per segment
-constexpr uint32_t kSlack = 8;                      // bytes in front of a lane's speculative symbols
-constexpr uint32_t kRegion = kSlack + kChunk + 4;   // lane scratch stride: 27 dwords, odd -> conflict-free
+constexpr uint32_t kSync = 24;                      // bits decoded before a chunk to synchronise
+constexpr uint32_t kRegion = kChunk + 4;            // lane symbol stride: 25 dwords, odd -> conflict-free
 constexpr uint32_t kSegBits = kWave * kChunk;       // 6144 bits per segment
 constexpr uint32_t kCarry = 256;                    // room for an unconsumed partial tile
 constexpr uint32_t kSymsBytes = kCarry + kWave * kRegion;
@@ -425,13 +426,14 @@ __device__ __forceinline__ uint32_t long_code(const Smem& S, uint32_t w, uint32_
   return (l << 8) | S.sorted[idx];
 }
 
-// A lane's decoded path through its chunk: codewords start at `start` and
-// run until `ex` (the first start at or past the chunk end); the `cnt`
-// symbols sit at region[base ...]; `mask` marks the path's starts within
-// [cs, cs + 32); `dead` = a window matched no code.
+// A lane's decoded chunk: `f` = its first codeword start at or past the chunk
+// start (kNoStart when the path failed before reaching it), `cnt` symbols at
+// region[0 ...], `ex` = the first start at or past the chunk end, `dead` = a
+// window in the chunk matched no code.
 struct Path {
-  uint32_t start, base, cnt, ex, mask, dead;
+  uint32_t f, cnt, ex, dead;
 };
+constexpr uint32_t kNoStart = 0xffffffffu;
 
 // Slide the register window (w0, w1, w2 = segment dwords (p+31)/32 - 1 ..
 // +1) after p advanced from `from` by at most 32 bits; the third dword is
@@ -445,36 +447,24 @@ __device__ __forceinline__ void slide(const Smem& S, uint32_t from, uint32_t p, 
   w2 = S.stream[i1 + 2];
 }
 
-// Up to two codewords at bit p (lut2 entry layout).  A window that matches no
-// code sets `dead` and moves p to ce, which ends the caller's loop.
-__device__ __forceinline__ uint32_t step2(const Smem& S, uint32_t& p, uint32_t ce, uint32_t& w0, uint32_t& w1,
+// Up to two codewords at bit p (lut2 entry layout); a second codeword that
+// would start at or past `end` is left for the caller.  A window that matches
+// no code sets `dead` and moves p to `end`, which ends the caller's loop.
+__device__ __forceinline__ uint32_t step2(const Smem& S, uint32_t& p, uint32_t end, uint32_t& w0, uint32_t& w1,
                                           uint32_t& w2, uint32_t maxlen, uint32_t& dead) {
   const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
   uint32_t e = S.t.f.lut2[win >> (32 - kLutBits)];
   if (e == 0) {
     const uint32_t lc = long_code(S, win, maxlen);
-    const uint32_t len = lc ? lc >> 8 : ce - p;
+    const uint32_t len = lc ? lc >> 8 : end - p;
     dead |= lc == 0;
     e = (lc & 255u) | (len << 16) | (len << 24);
   }
-  // A second codeword starting at or past ce belongs to the next chunk.
   const uint32_t l1 = (e >> 24) & 15u;
-  if (((e >> 23) & 1u) && p + l1 >= ce) e = (e & 0x0f0000ffu) | (l1 << 16);
+  const bool cut = ((e >> 23) & 1u) && p + l1 >= end;
+  e = cut ? (e & 0x0f0000ffu) | (l1 << 16) : e;
   const uint32_t from = p;
   p += (e >> 16) & 127u;
-  slide(S, from, p, w0, w1, w2);
-  return e;
-}
-
-// One codeword at bit p: (len << 8) | symbol, 0 if invalid.
-__device__ __forceinline__ uint32_t step1(const Smem& S, uint32_t& p, uint32_t& w0, uint32_t& w1, uint32_t& w2,
-                                          uint32_t maxlen) {
-  const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
-  const uint32_t e2 = S.t.f.lut2[win >> (32 - kLutBits)];
-  const uint32_t e = e2 ? (((e2 >> 24) & 15u) << 8) | (e2 & 255u) : long_code(S, win, maxlen);
-  if (e == 0) return 0;
-  const uint32_t from = p;
-  p += e >> 8;
   slide(S, from, p, w0, w1, w2);
   return e;
 }
@@ -486,65 +476,29 @@ __device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t&
   w2 = S.stream[i + 2];
 }
 
-// Decode codewords starting in [from, ce) into region[base ...], two per
-// lookup where the table allows.  Each store writes both symbol slots; the
-// count advances by the number present.
-__device__ __forceinline__ void decode_path(const Smem& S, uint32_t from, uint32_t cs, uint32_t ce, uint8_t* region,
-                                            uint32_t base, uint32_t maxlen, Path& P) {
-  uint32_t p = from, c = 0, m = 0, d = 0, w0, w1, w2;
+// Decode the codewords that start in [cs, ce) into region[0 ...], two per
+// lookup where the table allows.  When `from` < cs the codewords before cs
+// are decoded and dropped: Huffman codes resynchronise within a few
+// codewords, so a path started kSync bits early almost always meets the true
+// codeword boundaries before cs (the caller verifies it against the previous
+// lane's exit).  Symbols are stored a byte at a time (aligned LDS stores).
+__device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint32_t cs, uint32_t ce, uint8_t* region,
+                                             uint32_t maxlen, Path& P) {
+  uint32_t p = from, c = 0, d = 0, w0, w1, w2;
   load_window(S, p, w0, w1, w2);
-  uint8_t* out = region + base;
-  while (p < ce && p - cs < 32) {  // starts inside the synchronisation window
-    const uint32_t rel = p - cs;
-    const uint32_t e = step2(S, p, ce, w0, w1, w2, maxlen, d);
-    const uint32_t two = (e >> 23) & 1u, rel2 = rel + ((e >> 24) & 15u);
-    m |= (1u << rel) | (two && rel2 < 32 ? 1u << rel2 : 0u);
-    const uint16_t sy = (uint16_t)e;
-    __builtin_memcpy(out + c, &sy, 2);
-    c += 1 + two;
-  }
+  while (p < cs) step2(S, p, cs, w0, w1, w2, maxlen, d);
+  P.f = d ? kNoStart : p;
+  if (d) p = ce;
+  volatile uint8_t* out = region;
   while (p < ce) {
     const uint32_t e = step2(S, p, ce, w0, w1, w2, maxlen, d);
-    const uint16_t sy = (uint16_t)e;
-    __builtin_memcpy(out + c, &sy, 2);
+    out[c] = (uint8_t)e;
+    out[c + 1] = (uint8_t)(e >> 8);
     c += 1 + ((e >> 23) & 1u);
   }
-  P.start = from;
-  P.base = base;
   P.cnt = c;
   P.ex = p;
-  P.mask = m;
   P.dead = d;
-}
-
-// The true entry pe is not on the lane's speculative path: decode from pe
-// until the true path reaches one of the recorded starts (the paths agree
-// from there on), keep the speculative tail and splice the new codewords in
-// front of it using the slack bytes.  False when no merge happens within
-// the window or the slack (the caller then re-decodes the whole chunk).
-__device__ __forceinline__ bool merge_path(const Smem& S, uint32_t pe, uint32_t cs, uint32_t ce, uint8_t* region,
-                                           uint32_t maxlen, Path& P) {
-  if (P.base != kSlack || P.start != cs) return false;
-  uint32_t p = pe, k = 0, m = 0, w0, w1, w2;
-  load_window(S, p, w0, w1, w2);
-  for (;;) {
-    const uint32_t rel = p - cs;
-    if (rel >= 32 || p >= ce || k >= kSlack) return false;
-    if ((P.mask >> rel) & 1u) break;
-    const uint32_t e = step1(S, p, w0, w1, w2, maxlen);
-    if (e == 0) return false;
-    m |= 1u << rel;
-    region[k++] = (uint8_t)e;
-  }
-  const uint32_t rel = p - cs, below = (1u << rel) - 1u;
-  const uint32_t j = (uint32_t)__popc(P.mask & below);
-  const uint32_t dst = kSlack + j - k;
-  for (uint32_t q = k; q-- > 0;) region[dst + q] = region[q];
-  P.base = dst;
-  P.cnt = P.cnt - j + k;
-  P.start = pe;
-  P.mask = m | (P.mask & ~below);
-  return true;
 }
 
 // Inputs of a stream's first segment, loaded ahead of use: the stream
@@ -616,19 +570,19 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
     const uint32_t cs = lane * kChunk;
     const bool active = cs < lim_bits;
     const uint32_t ce = active ? min(cs + kChunk, lim_bits) : cs;
-    Path P{cs, kSlack, 0, cs, 0, 0};
-    if (active) decode_path(S, cs, cs, ce, region, kSlack, maxlen, P);
-    // Resolve: lane i is consistent when its predecessor's exit is a
-    // codeword start on lane i's path.  Lanes before the first
-    // inconsistent lane are on the true path.
+    // Lane 0 starts at the true entry; the others kSync bits before their chunk.
+    Path P{cs, 0, cs, 0};
+    if (active) decode_chunk(S, lane ? cs - kSync : entry, cs, ce, region, maxlen, P);
+    // Resolve: lane i is on the true path when its first start equals its
+    // predecessor's exit and the predecessor is.  Lanes that fail re-decode
+    // from that exit (rare: a path that did not resynchronise within kSync).
     for (;;) {
       uint32_t pe = from_prev_lane(P.ex), pd = from_prev_lane(P.dead);
       if (lane == 0) {
         pe = entry;
         pd = 0;
       }
-      const uint32_t off = pe - cs;
-      const bool ok = !active || (!pd && (pe == P.start || (off < 32 && ((P.mask >> off) & 1u))));
+      const bool ok = !active || (!pd && P.f == pe);
       const uint64_t bad = __ballot(!ok);
       const uint64_t deadm = __ballot(active && P.dead);
       const uint64_t resolved = bad ? ((1ull << (__ffsll((unsigned long long)bad) - 1)) - 1) : ~0ull;
@@ -637,15 +591,10 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
         break;
       }
       if (!bad) break;
-      if (!ok && !pd && !merge_path(S, pe, cs, ce, region, maxlen, P)) decode_path(S, pe, cs, ce, region, 0, maxlen, P);
+      if (!ok && !pd) decode_chunk(S, pe, cs, ce, region, maxlen, P);
     }
     if (err) break;
-    uint32_t pe = from_prev_lane(P.ex);
-    if (lane == 0) pe = entry;
-    const uint32_t off = pe - cs;
-    const uint32_t j = (!active || pe == P.start) ? 0u : (uint32_t)__popc(P.mask & ((1u << off) - 1u));
-    const uint32_t first = P.base + j;
-    const uint32_t t = active ? P.cnt - j : 0u;
+    const uint32_t t = active ? P.cnt : 0u;
     const uint32_t tinc = wave_incl(t, lane);
     const uint32_t total = rdlane(tinc, kWave - 1);
     const uint64_t act = __ballot(active);
@@ -655,30 +604,46 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
       err = kErrStream;  // more codewords than elements: trailing bits
       break;
     }
-    // Compact the lanes' runs behind the carried partial tile.
+    // Compact the lanes' runs behind the carried partial tile, with aligned
+    // LDS accesses only: a lane reads its run as aligned dwords, realigns
+    // them to the destination with byte funnel shifts, stores the whole
+    // destination dwords and writes the (at most 3 + 3) bytes it shares with
+    // its neighbours one at a time.  All reads precede all writes: a run's
+    // destination can overlap other lanes' sources.
     {
       const uint32_t dst = carry + tinc - t;
-      const uint32_t nd = (t + 3) >> 2, ndmax = wave_max(nd);
-      const uint32_t nfull = t >> 2, tail = t & 3u;
+      const uint32_t dh = dst & 3u, nq = (t + 3) >> 2, nqmax = wave_max(nq);
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(region);
       uint32_t R[kChunk / 4];
 #pragma unroll
       for (uint32_t q = 0; q < kChunk / 4; ++q) {
-        if (q >= ndmax) break;
-        R[q] = q < nd ? lds32(region + first + 4 * q) : 0u;
+        if (q >= nqmax) break;
+        R[q] = q < nq ? src[q] : 0u;
       }
       wave_sync();
+      uint32_t* d32 = reinterpret_cast<uint32_t*>(S.syms + (dst & ~3u));
+      const uint32_t sh = (4u - dh) & 3u;  // destination dword k = run bytes [4k - dh, 4k - dh + 4)
+      const uint32_t nw = (dh + t) >> 2;   // destination dwords that end inside the run
+      uint32_t head = 0, tail = 0, prev = 0;
 #pragma unroll
-      for (uint32_t q = 0; q < kChunk / 4; ++q) {
-        if (q >= ndmax) break;
-        uint8_t* p = S.syms + dst + 4 * q;
-        if (q < nfull) {
-          sts32(p, R[q]);
-        } else if (q == nfull && tail) {
-          p[0] = (uint8_t)R[q];
-          if (tail > 1) p[1] = (uint8_t)(R[q] >> 8);
-          if (tail > 2) p[2] = (uint8_t)(R[q] >> 16);
-        }
+      for (uint32_t k = 0; k <= kChunk / 4; ++k) {
+        if (k > nqmax) break;
+        const uint32_t cur = k < nq ? R[k < kChunk / 4 ? k : 0] : 0u;
+        const uint32_t w = dh ? __builtin_amdgcn_alignbyte(cur, prev, sh) : cur;
+        if (k == 0) head = w;
+        if (k == nw) tail = w;
+        if (k < nw && (k > 0 || dh == 0)) d32[k] = w;
+        prev = cur;
       }
+      volatile uint8_t* d8 = S.syms + (dst & ~3u);
+      // Head: bytes dh..3 of dword 0 (when the run does not start aligned).
+#pragma unroll
+      for (uint32_t b = 1; b < 4; ++b)
+        if (dh && b >= dh && b - dh < t) d8[b] = (uint8_t)(head >> (8 * b));
+      // Tail: bytes 0..(dh + t) % 4 - 1 of dword nw, unless that is the head dword.
+#pragma unroll
+      for (uint32_t b = 0; b < 3; ++b)
+        if ((nw > 0 || dh == 0) && b < ((dh + t) & 3u)) d8[4 * nw + b] = (uint8_t)(tail >> (8 * b));
       wave_sync();
     }
     const uint32_t avail = carry + total;
