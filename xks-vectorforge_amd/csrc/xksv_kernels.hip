@@ -176,6 +176,12 @@ __device__ __forceinline__ uint32_t lds32(const uint8_t* p) {
   return v;
 }
 __device__ __forceinline__ void sts32(uint8_t* p, uint32_t v) { __builtin_memcpy(p, &v, 4); }
+// Byte stores into LDS that the compiler must keep as single-byte DS stores
+// (merged neighbours would be misaligned wider stores).  The explicit LDS
+// address space keeps them DS instructions: a volatile generic pointer would
+// become FLAT.
+typedef __attribute__((address_space(3))) volatile uint8_t* lds_bytes;
+__device__ __forceinline__ lds_bytes as_lds(uint8_t* p) { return (lds_bytes)p; }
 __device__ __forceinline__ uint32_t bswap32(uint32_t v) { return __builtin_amdgcn_perm(0u, v, 0x00010203u); }
 
 // Eight exponents (E, little-endian byte i = element i) and eight
@@ -489,7 +495,7 @@ __device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint3
   while (p < cs) step2(S, p, cs, w0, w1, w2, maxlen, d);
   P.f = d ? kNoStart : p;
   if (d) p = ce;
-  volatile uint8_t* out = region;
+  lds_bytes out = as_lds(region);
   while (p < ce) {
     const uint32_t e = step2(S, p, ce, w0, w1, w2, maxlen, d);
     out[c] = (uint8_t)e;
@@ -635,7 +641,7 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
         if (k < nw && (k > 0 || dh == 0)) d32[k] = w;
         prev = cur;
       }
-      volatile uint8_t* d8 = S.syms + (dst & ~3u);
+      lds_bytes d8 = as_lds(S.syms + (dst & ~3u));
       // Head: bytes dh..3 of dword 0 (when the run does not start aligned).
 #pragma unroll
       for (uint32_t b = 1; b < 4; ++b)
