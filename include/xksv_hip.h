@@ -79,6 +79,14 @@ int xksv_hip_gemv_parallel(const void* input, size_t n, const float* x, float* o
  * the layout of xksv_cuda_gemm. */
 int xksv_hip_gemm_parallel(const void* input, size_t n, size_t batch, const float* x, float* output);
 
+/* No reference counterpart (the reference's GEMM takes fp32 X only): fused
+ * decode-GEMM over an XKSP2 block with bf16 activations in the layout of
+ * torch's x @ W.T -- X [batch, cols] bf16 row-major, output [batch, rows] fp32
+ * row-major -- accumulated in fp32.  From batch 8, when every substream covers
+ * whole 16x16 tiles, the products run on bf16 MFMA (v_mfma_f32_16x16x32_bf16);
+ * below that on fp32 VALU FMAs. */
+int xksv_hip_gemm_parallel_bf16(const void* input, size_t n, size_t batch, const uint16_t* x, float* output);
+
 /* Reference names, same functions. */
 int xksv_cuda_decode(const void* input, size_t size, size_t rows, size_t cols, void* output);
 int xksv_cuda_gemv(const void* input, size_t size, size_t rows, size_t cols, const float* x, float* output);
@@ -128,6 +136,12 @@ int xksv_hip_plan_decode(xksv_hip_plan* plan, const void* archive, void* out, ui
  * is the batch-1 GEMV of python/runtime.py:264-284. */
 int xksv_hip_plan_gemm(xksv_hip_plan* plan, const void* archive, const float* x, size_t batch, float* y,
                        void* stream);
+
+/* As xksv_hip_plan_gemm with bf16 activations X [batch, cols] row-major and
+ * fp32 output Y [batch, M] row-major, M = the plan's row extent (largest
+ * out_offset + rows); bf16 MFMA from batch 8 (see xksv_hip_gemm_parallel_bf16). */
+int xksv_hip_plan_gemm_bf16(xksv_hip_plan* plan, const void* archive, const uint16_t* x, size_t batch, float* y,
+                            void* stream);
 
 /* Synchronize `stream`, return the number of failed blocks (or -1 on a HIP
  * error); *first_bad (optional) gets the first failing block index or -1,

@@ -93,28 +93,35 @@ void release(int dev, Buf b) {
   g_pool[dev].push_back(b);
 }
 
-// Staging layout for one block: [2 descriptors][status][counter][partials][block][scratch].
+// Staging layout for one block: [2 descriptors][status][block][scratch].
 struct Layout {
-  uint64_t desc = 0, status, counters, partial, block, scratch, total;
+  uint64_t desc = 0, status, block, scratch, total;
   Layout(uint64_t block_size, uint64_t scratch_size) {
     status = align_up(desc + 2 * sizeof(DevBlock), kAlign);
-    counters = status + kAlign;
-    partial = counters + kAlign;
-    block = align_up(partial + (uint64_t)kMaxChunks * 16 * kMaxFusedBatch * sizeof(float), kAlign);
+    block = status + kAlign;
     scratch = align_up(block + block_size + 16, kAlign);
     total = scratch + align_up(scratch_size, kAlign);
   }
 };
 
-// One block through the GPU.  mode 0: decode into `out` (device); mode 1:
-// fused GEMM with fp32 X[cols, batch] into Y[rows, batch].
-int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows, uint64_t cols, bool fused_ok,
-              int mode, void* out, const float* x, uint64_t batch) {
+// What a block-level call computes.  kDecode: BF16 into `out` (device).
+// kGemmF32: fused GEMM with fp32 X [cols, batch] into Y [rows, batch].
+// kGemmBf16: fused GEMM with bf16 X [batch, cols] into fp32 Y [batch, rows]
+// (bf16 MFMA from batch 8 when every substream covers whole tiles).
+enum Mode { kDecode, kGemmF32, kGemmBf16 };
+struct Fused {
+  bool unit = false;  // every stream unit-aligned: fused consumers apply
+  bool tile = false;  // every stream covers whole 16x16 tiles: MFMA applies
+};
+
+// One block through the GPU.
+int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows, uint64_t cols, Fused fused,
+              Mode mode, void* out, const void* x, uint64_t batch) {
   int dev = -1;
   const DeviceInfo* di = current_device(&dev);
   if (!di) return 1;
   const uint64_t n = rows * cols;
-  const bool generic_gemm = mode == 1 && !fused_ok;
+  const bool generic_gemm = mode != kDecode && !fused.unit;
   Layout L(size, generic_gemm ? n * 2 : 0);
   Buf b;
   if (!acquire(dev, L.total, b)) return 1;
@@ -126,29 +133,35 @@ int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows
     if (hipMemcpy(b.p + L.desc, d, sizeof d, hipMemcpyHostToDevice) != hipSuccess) break;
     if (hipMemcpy(b.p + L.block, input, size, hipMemcpyHostToDevice) != hipSuccess) break;
     uint32_t* status = reinterpret_cast<uint32_t*>(b.p + L.status);
-    if (launch_fill_u32(status, (L.partial - L.status) / 4, 0, nullptr) != hipSuccess) break;
+    if (launch_fill_u32(status, kAlign / 4, 0, nullptr) != hipSuccess) break;
     const DevBlock* dd = reinterpret_cast<const DevBlock*>(b.p + L.desc);
-    if (mode == 0) {
-      if (launch_decode(dd, 1, codec, b.p, static_cast<uint8_t*>(out), status, nullptr, (unsigned)di->cus,
-                        nullptr) != hipSuccess)
+    const unsigned cus = (unsigned)di->cus;
+    float* y = static_cast<float*>(out);
+    if (mode == kDecode) {
+      if (launch_decode(dd, 1, codec, b.p, static_cast<uint8_t*>(out), status, nullptr, cus, nullptr) != hipSuccess)
         break;
     } else if (!generic_gemm) {
       bool ok = true;
       for (uint64_t j0 = 0; j0 < batch && ok; j0 += kMaxFusedBatch) {
         const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
-        ok = launch_gemm_f32(dd, 1, codec, b.p, x + j0, batch, nb, static_cast<float*>(out) + j0, batch, status,
-                             reinterpret_cast<float*>(b.p + L.partial),
-                             reinterpret_cast<uint32_t*>(b.p + L.counters), (unsigned)di->cus, nullptr) == hipSuccess;
+        if (mode == kGemmF32)
+          ok = launch_gemm_f32(dd, 1, codec, b.p, static_cast<const float*>(x) + j0, batch, nb, y + j0, batch, status,
+                               cus, nullptr) == hipSuccess;
+        else
+          ok = launch_gemm_bf16(dd, 1, codec, b.p, static_cast<const uint16_t*>(x) + j0 * cols, cols, nb,
+                                y + j0 * rows, rows, fused.tile, status, cus, nullptr) == hipSuccess;
       }
       if (!ok) break;
     } else {
       // Not unit-aligned: decode to scratch, then a plain deterministic GEMM.
-      if (launch_decode(dd, 1, codec, b.p, b.p + L.scratch, status, nullptr, (unsigned)di->cus, nullptr) !=
-          hipSuccess)
-        break;
-      if (launch_gemm_plain(dd + 1, 1, b.p, x, batch, (uint32_t)batch, static_cast<float*>(out), batch, nullptr) !=
-          hipSuccess)
-        break;
+      if (launch_decode(dd, 1, codec, b.p, b.p + L.scratch, status, nullptr, cus, nullptr) != hipSuccess) break;
+      const hipError_t e =
+          mode == kGemmF32
+              ? launch_gemm_plain(dd + 1, 1, b.p, static_cast<const float*>(x), batch, (uint32_t)batch, y, batch,
+                                  nullptr)
+              : launch_gemm_plain_bf16(dd + 1, 1, b.p, static_cast<const uint16_t*>(x), cols, (uint32_t)batch, y,
+                                       rows, nullptr);
+      if (e != hipSuccess) break;
     }
     if (hipStreamSynchronize(nullptr) != hipSuccess) break;
     uint32_t st = 1;
@@ -176,15 +189,25 @@ bool parallel_header(const uint8_t* p, uint64_t n, ParallelHeader& h) {
 }
 
 // Fused kernels need 16-row slabs of whole tiles whose streams start and end
-// on 8-element boundaries.
-bool fused_parallel_ok(const ParallelHeader& h) {
-  if (h.rows != 16 || h.cols % 16) return false;
+// on 8-element boundaries; the MFMA consumer needs them on tile boundaries.
+Fused fused_parallel(const ParallelHeader& h) {
+  Fused f;
+  if (h.rows != 16 || h.cols % 16) return f;
   const uint64_t total = h.rows * h.cols;
-  for (uint64_t k = 0; k <= h.chunks; ++k)
-    if ((total * k / h.chunks) % 8) return false;
-  return true;
+  f.unit = f.tile = true;
+  for (uint64_t k = 0; k <= h.chunks; ++k) {
+    const uint64_t b = total * k / h.chunks;
+    f.unit = f.unit && b % 8 == 0;
+    f.tile = f.tile && b % 256 == 0;
+  }
+  f.tile = f.tile && f.unit;
+  return f;
 }
-bool fused_serial_ok(uint64_t rows, uint64_t cols) { return rows == 16 && cols % 16 == 0; }
+Fused fused_serial(uint64_t rows, uint64_t cols) {
+  Fused f;
+  f.unit = f.tile = rows == 16 && cols % 16 == 0;
+  return f;
+}
 
 // Oversubscription of a lengths table, as the reference's canonical()
 // detects it (src/codec.cpp:20-22): some length has more codes than free slots.
@@ -219,7 +242,7 @@ int unpack_via_gpu(const uint8_t* p, uint64_t n, uint32_t codec, uint64_t rows, 
   const uint64_t bytes = rows * cols * 2;
   Buf b;
   if (!acquire(dev, align_up(bytes, kAlign) + 64, b)) return -1;
-  int rc = run_block(p, n, codec, rows, cols, false, 0, b.p, nullptr, 0) ? -1 : to_host(b.p, bytes, out, out_size);
+  int rc = run_block(p, n, codec, rows, cols, Fused{}, kDecode, b.p, nullptr, 0) ? -1 : to_host(b.p, bytes, out, out_size);
   release(dev, b);
   return rc;
 }
@@ -245,9 +268,8 @@ struct xksv_hip_plan {
   DevBlock *g_fserial = nullptr, *g_fparallel = nullptr, *g_gser = nullptr, *g_gpar = nullptr, *g_gplain = nullptr,
            *g_raw = nullptr;
   uint32_t n_fserial = 0, n_fparallel = 0, n_gser = 0, n_gpar = 0, n_generic = 0, n_graw = 0;
+  bool tile_parallel = false;  // parallel32 slabs split into whole-tile substreams (MFMA consumer)
   uint8_t* scratch = nullptr;
-  float* partial = nullptr;
-  uint32_t* counters = nullptr;
   std::vector<uint32_t> h_status;
 };
 
@@ -305,15 +327,10 @@ bool prepare_gemm(xksv_hip_plan* P) {
   P->n_gpar = (uint32_t)gdp.size();
   P->n_generic = (uint32_t)gp.size();
   P->n_graw = (uint32_t)raw.size();
+  // The reference's encoder splits a 16-row slab into 32 substreams of 16 *
+  // cols / 32 elements: whole tiles when cols is a multiple of 512.
+  P->tile_parallel = cols % 512 == 0;
   if (scratch && hipMalloc(reinterpret_cast<void**>(&P->scratch), scratch) != hipSuccess) return false;
-  if (P->n_fparallel) {
-    const uint64_t nparts = (uint64_t)P->n_fparallel * kMaxChunks * 16 * kMaxFusedBatch;
-    if (hipMalloc(reinterpret_cast<void**>(&P->partial), nparts * sizeof(float)) != hipSuccess) return false;
-    if (hipMalloc(reinterpret_cast<void**>(&P->counters), P->n_fparallel * sizeof(uint32_t)) != hipSuccess)
-      return false;
-    if (launch_fill_u32(P->counters, P->n_fparallel, 0, nullptr) != hipSuccess) return false;
-    if (hipStreamSynchronize(nullptr) != hipSuccess) return false;
-  }
   P->gemm_valid = true;
   return true;
 }
@@ -335,7 +352,7 @@ int xksv_hip_decode(const void* input, size_t size, size_t rows, size_t cols, vo
   const uint8_t* p = static_cast<const uint8_t*>(input);
   if (!p || !output || size < 272 || !rows || !cols || cols > SIZE_MAX / rows) return 1;
   if (rows * cols > kMaxBlockElems) return 1;
-  return run_block(p, size, kCodecSerial, rows, cols, false, 0, output, nullptr, 0);
+  return run_block(p, size, kCodecSerial, rows, cols, Fused{}, kDecode, output, nullptr, 0);
 }
 
 int xksv_hip_gemm(const void* input, size_t size, size_t rows, size_t cols, size_t batch, const float* x,
@@ -345,7 +362,7 @@ int xksv_hip_gemm(const void* input, size_t size, size_t rows, size_t cols, size
       batch > SIZE_MAX / rows || batch > SIZE_MAX / cols)
     return 1;
   if (rows * cols > kMaxBlockElems) return 1;
-  return run_block(p, size, kCodecSerial, rows, cols, fused_serial_ok(rows, cols), 1, output, x, batch);
+  return run_block(p, size, kCodecSerial, rows, cols, fused_serial(rows, cols), kGemmF32, output, x, batch);
 }
 
 int xksv_hip_gemv(const void* input, size_t size, size_t rows, size_t cols, const float* x, float* output) {
@@ -355,16 +372,24 @@ int xksv_hip_gemv(const void* input, size_t size, size_t rows, size_t cols, cons
 int xksv_hip_decode_parallel(const void* input, size_t n, void* output) {
   ParallelHeader h;
   if (!output || !parallel_header(static_cast<const uint8_t*>(input), n, h)) return 1;
-  return run_block(static_cast<const uint8_t*>(input), n, kCodecParallel, h.rows, h.cols, false, 0, output, nullptr,
-                   0);
+  return run_block(static_cast<const uint8_t*>(input), n, kCodecParallel, h.rows, h.cols, Fused{}, kDecode, output,
+                   nullptr, 0);
 }
 
 int xksv_hip_gemm_parallel(const void* input, size_t n, size_t batch, const float* x, float* output) {
   ParallelHeader h;
   if (!x || !output || !batch || !parallel_header(static_cast<const uint8_t*>(input), n, h)) return 1;
   if (batch > SIZE_MAX / h.rows) return 1;
-  return run_block(static_cast<const uint8_t*>(input), n, kCodecParallel, h.rows, h.cols, fused_parallel_ok(h), 1,
+  return run_block(static_cast<const uint8_t*>(input), n, kCodecParallel, h.rows, h.cols, fused_parallel(h), kGemmF32,
                    output, x, batch);
+}
+
+int xksv_hip_gemm_parallel_bf16(const void* input, size_t n, size_t batch, const uint16_t* x, float* output) {
+  ParallelHeader h;
+  if (!x || !output || !batch || !parallel_header(static_cast<const uint8_t*>(input), n, h)) return 1;
+  if (batch > SIZE_MAX / h.rows || batch > SIZE_MAX / h.cols) return 1;
+  return run_block(static_cast<const uint8_t*>(input), n, kCodecParallel, h.rows, h.cols, fused_parallel(h),
+                   kGemmBf16, output, x, batch);
 }
 
 int xksv_hip_gemv_parallel(const void* input, size_t n, const float* x, float* output) {
@@ -463,7 +488,7 @@ int xksv_hip_plan_destroy(xksv_hip_plan* P) {
   if (P->device >= 0 && cur != P->device) (void)hipSetDevice(P->device);
   for (void* p : {(void*)P->d_serial, (void*)P->d_parallel, (void*)P->d_raw, (void*)P->status, (void*)P->g_fserial,
                   (void*)P->g_fparallel, (void*)P->g_gser, (void*)P->g_gpar, (void*)P->g_gplain, (void*)P->g_raw,
-                  (void*)P->scratch, (void*)P->partial, (void*)P->counters})
+                  (void*)P->scratch})
     if (p) (void)hipFree(p);
   if (cur >= 0 && cur != P->device) (void)hipSetDevice(cur);
   delete P;
@@ -489,33 +514,66 @@ int xksv_hip_plan_decode(xksv_hip_plan* P, const void* archive, void* out, uint6
   return 0;
 }
 
-int xksv_hip_plan_gemm(xksv_hip_plan* P, const void* archive, const float* x, size_t batch, float* y,
-                       void* stream) {
+// The plan GEMMs: fused kernels over 16-row compressed slabs, decode to
+// scratch + plain GEMM for other compressed slabs, plain GEMM straight from
+// the archive for raw slabs.  bf16 == false: fp32 X [cols, batch], Y
+// [rows, batch]; bf16 == true: bf16 X [batch, cols], fp32 Y [batch, rows].
+static int plan_gemm(xksv_hip_plan* P, const void* archive, const void* x, size_t batch, float* y, void* stream,
+                     bool bf16) {
   if (!P || !archive || !x || !y || !batch) return 1;
   const DeviceInfo* di = current_device(nullptr);
   if (!di || !prepare_gemm(P)) return 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* arc = static_cast<const uint8_t*>(archive);
+  const unsigned cus = (unsigned)di->cus;
   uint32_t* queue = P->status + P->blocks.size();
+  const float* xf = static_cast<const float*>(x);
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const uint64_t M = P->rows_extent, K = P->cols;
   if (launch_fill_u32(P->status, P->blocks.size() + kQueues, 0, s) != hipSuccess) return 1;
   for (uint64_t j0 = 0; j0 < batch; j0 += kMaxFusedBatch) {
     const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
-    if (launch_gemm_f32(P->g_fparallel, P->n_fparallel, kCodecParallel, arc, x + j0, batch, nb, y + j0, batch,
-                        P->status, P->partial, P->counters, (unsigned)di->cus, s) != hipSuccess)
+    hipError_t e1, e2;
+    if (!bf16) {
+      e1 = launch_gemm_f32(P->g_fparallel, P->n_fparallel, kCodecParallel, arc, xf + j0, batch, nb, y + j0, batch,
+                           P->status, cus, s);
+      e2 = launch_gemm_f32(P->g_fserial, P->n_fserial, kCodecSerial, arc, xf + j0, batch, nb, y + j0, batch,
+                           P->status, cus, s);
+    } else {
+      e1 = launch_gemm_bf16(P->g_fparallel, P->n_fparallel, kCodecParallel, arc, xb + j0 * K, K, nb, y + j0 * M, M,
+                            P->tile_parallel, P->status, cus, s);
+      e2 = launch_gemm_bf16(P->g_fserial, P->n_fserial, kCodecSerial, arc, xb + j0 * K, K, nb, y + j0 * M, M, true,
+                            P->status, cus, s);
+    }
+    if (e1 != hipSuccess || e2 != hipSuccess) return 1;
+  }
+  if (launch_decode(P->g_gser, P->n_gser, kCodecSerial, arc, P->scratch, P->status, queue + 2, cus, s) !=
+          hipSuccess ||
+      launch_decode(P->g_gpar, P->n_gpar, kCodecParallel, arc, P->scratch, P->status, queue + 3, cus, s) !=
+          hipSuccess)
+    return 1;
+  if (!bf16) {
+    if (launch_gemm_plain(P->g_gplain, P->n_generic, P->scratch, xf, batch, (uint32_t)batch, y, batch, s) !=
+            hipSuccess ||
+        launch_gemm_plain(P->g_raw, P->n_graw, arc, xf, batch, (uint32_t)batch, y, batch, s) != hipSuccess)
       return 1;
-    if (launch_gemm_f32(P->g_fserial, P->n_fserial, kCodecSerial, arc, x + j0, batch, nb, y + j0, batch, P->status,
-                        P->partial, P->counters, (unsigned)di->cus, s) != hipSuccess)
+  } else {
+    if (launch_gemm_plain_bf16(P->g_gplain, P->n_generic, P->scratch, xb, K, (uint32_t)batch, y, M, s) !=
+            hipSuccess ||
+        launch_gemm_plain_bf16(P->g_raw, P->n_graw, arc, xb, K, (uint32_t)batch, y, M, s) != hipSuccess)
       return 1;
   }
-  if (launch_decode(P->g_gser, P->n_gser, kCodecSerial, arc, P->scratch, P->status, queue + 2, (unsigned)di->cus, s) !=
-          hipSuccess ||
-      launch_decode(P->g_gpar, P->n_gpar, kCodecParallel, arc, P->scratch, P->status, queue + 3, (unsigned)di->cus,
-                    s) != hipSuccess)
-    return 1;
-  if (launch_gemm_plain(P->g_gplain, P->n_generic, P->scratch, x, batch, (uint32_t)batch, y, batch, s) != hipSuccess)
-    return 1;
-  if (launch_gemm_plain(P->g_raw, P->n_graw, arc, x, batch, (uint32_t)batch, y, batch, s) != hipSuccess) return 1;
   return 0;
+}
+
+int xksv_hip_plan_gemm(xksv_hip_plan* P, const void* archive, const float* x, size_t batch, float* y,
+                       void* stream) {
+  return plan_gemm(P, archive, x, batch, y, stream, false);
+}
+
+int xksv_hip_plan_gemm_bf16(xksv_hip_plan* P, const void* archive, const uint16_t* x, size_t batch, float* y,
+                            void* stream) {
+  return plan_gemm(P, archive, x, batch, y, stream, true);
 }
 
 int64_t xksv_hip_plan_errors(xksv_hip_plan* P, void* stream, int64_t* first_bad, uint32_t* bits) {

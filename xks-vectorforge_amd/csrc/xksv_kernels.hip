@@ -516,7 +516,7 @@ struct StreamIn {
   uint4 bits;
 };
 // Sign/mantissa bytes of the first 256 units (2048 positions) a consume call
-// will see: unit lane + 64 i in v[i].
+// will see: unit lane_unit(lane) + 64 i in v[i] (the consumer's own mapping).
 struct SmWin {
   uint64_t v[4];
 };
@@ -531,10 +531,10 @@ __device__ __forceinline__ void issue_stream(StreamIn& P, const uint8_t* seg, co
   P.bits = lane < kStreamLanes ? ldg16_bounded(seg + 272 + (uint64_t)count + 16 * lane, seg_end)
                                : make_uint4(0u, 0u, 0u, 0u);
 }
-__device__ __forceinline__ void issue_sm(SmWin& W, const uint8_t* sm, uint32_t pos0, uint32_t count, uint32_t lane) {
+__device__ __forceinline__ void issue_sm(SmWin& W, const uint8_t* sm, uint32_t pos0, uint32_t count, uint32_t lu) {
 #pragma unroll
   for (uint32_t i = 0; i < 4; ++i) {
-    const uint32_t p = pos0 + 8 * (lane + kWave * i);
+    const uint32_t p = pos0 + 8 * (lu + kWave * i);
     W.v[i] = p + 8 <= count ? ldg64(sm + p) : 0ull;
   }
 }
@@ -570,7 +570,7 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
     if (S0 + kSegBits < nbits && lane < kStreamLanes)
       cur = ldg16_bounded(st.bits + ((S0 + kSegBits) >> 3) + 16 * lane, bend);
     SmWin W;
-    issue_sm(W, st.sm, pos0, st.count, lane);
+    issue_sm(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
     const uint64_t left = nbits - S0;
     const uint32_t lim_bits = left < kSegBits ? (uint32_t)left : kSegBits;
     const uint32_t cs = lane * kChunk;
@@ -714,7 +714,7 @@ __device__ __forceinline__ uint32_t decode_slow(Smem& S, uint32_t lane, const St
     wave_sync();
     if (err) break;
     SmWin W;
-    issue_sm(W, st.sm, produced, st.count, lane);
+    issue_sm(W, st.sm, produced, st.count, Cons::lane_unit(lane));
     C.consume(S, lane, st, produced, nseg, produced + nseg == st.count, W);
     wave_sync();
     produced += nseg;
@@ -765,6 +765,7 @@ struct Writer {
   uint64_t rows, cols;
   uint32_t tpb;  // tiles per 16-row band
   bool aligned;
+  static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) { return lane; }
   __device__ __forceinline__ void unit(const Smem& S, const Stream& st, uint32_t pos0, uint32_t u, uint64_t M) const {
     uint64_t E;
     __builtin_memcpy(&E, S.syms + 8 * u, 8);
@@ -800,16 +801,37 @@ struct Writer {
   }
 };
 
-// Fused GEMM over unit-aligned streams of 16-row slabs, fp32 activations
-// X[c * ldx + j] (cuda/decode.cu:94 layout, batch columns j < nb).  Lane
-// `lane` accumulates unit u = lane + 64 i of every consume call; its row is
-// ((start / 8 + lane) / 2) % 16 for the whole stream.
+// Fused GEMM consumers.  Each one accumulates one wave's share of a 16-row
+// slab's Y = W X and, after every stream, adds it into the wave's LDS slots
+// (kOut floats: 16 rows x kCols batch columns); the kernel sums the waves'
+// slots in wave order and stores them through store().
+struct GemmArgs {
+  const void* x;
+  uint64_t ldx;  // X row stride in elements
+  uint32_t nb;   // batch columns of this launch (<= kCols)
+  float* y;
+  uint64_t ldy;  // Y row stride in elements
+};
+
+// fp32 activations X[c * ldx + j] (cuda/decode.cu:94 layout), Y[(dst + r) *
+// ldy + j]; VALU FMAs.  Lane `lane` accumulates unit u = lane + 64 i of every
+// consume call; its row is ((start / 8 + lane) / 2) % 16 for the whole stream.
 template <int NB>
 struct GemmF32 {
+  static constexpr int kCols = NB, kOut = 16 * NB;
   const float* x;
   uint64_t ldx;
   uint32_t nb;
   float acc[NB];
+  __device__ __forceinline__ explicit GemmF32(const GemmArgs& a)
+      : x(static_cast<const float*>(a.x)), ldx(a.ldx), nb(a.nb) {}
+  static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) { return lane; }
+  static __device__ __forceinline__ bool fits(uint32_t s0, uint32_t count, uint64_t rows, uint64_t cols) {
+    return unit_aligned(s0, count, rows, cols);
+  }
+  static __device__ __forceinline__ void store(const GemmArgs& a, uint64_t dst, uint32_t r, uint32_t j, float v) {
+    if (j < a.nb) a.y[(dst + r) * a.ldy + j] = v;
+  }
   __device__ __forceinline__ void init() {
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = 0.f;
@@ -846,8 +868,8 @@ struct GemmF32 {
       }
     }
   }
-  __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final,
-                              const SmWin& W) {
+  __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0,
+                                              uint32_t avail, bool final, const SmWin& W) {
     const uint32_t take = final ? avail : (avail & ~255u);
     const uint32_t units = take >> 3;
 #pragma unroll
@@ -860,14 +882,157 @@ struct GemmF32 {
   }
   // Four lanes share each row: with s = (stream start / 8) % 2, lane l and
   // ((l + s) ^ 1) - s (mod 64) hold the two halves of a tile row, and l ^ 32
-  // the same row two tiles on.  After the two exchanges all four hold the sum.
-  __device__ __forceinline__ void reduce(uint32_t lane, uint32_t s) {
-    const int partner = (int)((((lane + s) ^ 1u) - s) & 63u);
+  // the same row two tiles on.  After the two exchanges all four hold the
+  // sum; one of them adds it to the slots.
+  __device__ __forceinline__ void deposit(float* slots, uint32_t lane, uint32_t s0) {
+    const uint32_t su = (s0 >> 3) & 1u;
+    const int partner = (int)((((lane + su) ^ 1u) - su) & 63u);
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       acc[j] += __shfl(acc[j], partner, kWave);
       acc[j] += __shfl_xor(acc[j], 32, kWave);
     }
+    const uint32_t row = (((s0 >> 3) + lane) >> 1) & 15u;
+    if (lane < 32 && ((lane + su) & 1u) == 0)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) slots[row * NB + j] += acc[j];
+  }
+};
+
+// bf16 activations in the layout of x @ W.T: X[j * ldx + c] (batch rows),
+// Y[j * ldy + dst + r]; VALU FMAs in fp32 (batch < 8).  Same lane mapping as
+// GemmF32.
+template <int NB>
+struct GemmBf16 {
+  static constexpr int kCols = NB, kOut = 16 * NB;
+  const uint16_t* x;
+  uint64_t ldx;
+  uint32_t nb;
+  float acc[NB];
+  __device__ __forceinline__ explicit GemmBf16(const GemmArgs& a)
+      : x(static_cast<const uint16_t*>(a.x)), ldx(a.ldx), nb(a.nb) {}
+  static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) { return lane; }
+  static __device__ __forceinline__ bool fits(uint32_t s0, uint32_t count, uint64_t rows, uint64_t cols) {
+    return unit_aligned(s0, count, rows, cols);
+  }
+  static __device__ __forceinline__ void store(const GemmArgs& a, uint64_t dst, uint32_t r, uint32_t j, float v) {
+    if (j < a.nb) a.y[j * a.ldy + dst + r] = v;
+  }
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j] = 0.f;
+  }
+  __device__ __forceinline__ void unit(const Smem& S, const Stream& st, uint32_t pos0, uint32_t u, uint64_t M) {
+    uint64_t E;
+    __builtin_memcpy(&E, S.syms + 8 * u, 8);
+    const uint4 w = combine8(E, M);
+    const uint32_t U = ((st.start + pos0) >> 3) + u;
+    const uint64_t col = 16ull * (U >> 5) + 8u * (U & 1u);
+    const float f[8] = {bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y),
+                        bf_lo(w.z), bf_hi(w.z), bf_lo(w.w), bf_hi(w.w)};
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (j >= (int)nb) break;
+      uint4 xv;
+      __builtin_memcpy(&xv, x + j * ldx + col, 16);
+      float a = acc[j];
+      a = fmaf(f[0], bf_lo(xv.x), a);
+      a = fmaf(f[1], bf_hi(xv.x), a);
+      a = fmaf(f[2], bf_lo(xv.y), a);
+      a = fmaf(f[3], bf_hi(xv.y), a);
+      a = fmaf(f[4], bf_lo(xv.z), a);
+      a = fmaf(f[5], bf_hi(xv.z), a);
+      a = fmaf(f[6], bf_lo(xv.w), a);
+      a = fmaf(f[7], bf_hi(xv.w), a);
+      acc[j] = a;
+    }
+  }
+  __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0,
+                                              uint32_t avail, bool final, const SmWin& W) {
+    const uint32_t take = final ? avail : (avail & ~255u);
+    const uint32_t units = take >> 3;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint32_t u = lane + kWave * i;
+      if (u < units) unit(S, st, pos0, u, W.v[i]);
+    }
+    for (uint32_t u = lane + 4 * kWave; u < units; u += kWave) unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
+    return take;
+  }
+  __device__ __forceinline__ void deposit(float* slots, uint32_t lane, uint32_t s0) {
+    const uint32_t su = (s0 >> 3) & 1u;
+    const int partner = (int)((((lane + su) ^ 1u) - su) & 63u);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      acc[j] += __shfl(acc[j], partner, kWave);
+      acc[j] += __shfl_xor(acc[j], 32, kWave);
+    }
+    const uint32_t row = (((s0 >> 3) + lane) >> 1) & 15u;
+    if (lane < 32 && ((lane + su) & 1u) == 0)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) slots[row * NB + j] += acc[j];
+  }
+};
+
+// bf16 activations (layout of GemmBf16), bf16 MFMA with fp32 accumulation
+// (batch 8..16, padded to 16): v_mfma_f32_16x16x32_bf16 multiplies a 16 x 32
+// slice of W (two 16x16 tiles side by side) by a 32 x 16 slice of X.  Lane
+// l = r + 16 g supplies W row r, columns 8g..8g+7 of the slice -- exactly one
+// decoded unit (half a tile row, unit 32 (g / 2) + 2 r + g % 2 of the tile
+// pair) -- and X rows (batch) l % 16 of the same 8 columns; it accumulates
+// Y rows 4 g .. 4 g + 3 of batch column l % 16.  Streams must cover whole
+// tiles.
+struct GemmMfma {
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  static constexpr int kCols = 16, kOut = 256;
+  const uint16_t* x;
+  uint64_t ldx;
+  uint32_t nb;
+  f32x4 acc;
+  __device__ __forceinline__ explicit GemmMfma(const GemmArgs& a)
+      : x(static_cast<const uint16_t*>(a.x)), ldx(a.ldx), nb(a.nb) {}
+  static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) {
+    const uint32_t r = lane & 15u, g = lane >> 4;
+    return 32u * (g >> 1) + 2u * r + (g & 1u);
+  }
+  static __device__ __forceinline__ bool fits(uint32_t s0, uint32_t count, uint64_t rows, uint64_t cols) {
+    return rows == 16 && cols % 16 == 0 && s0 % 256 == 0 && count % 256 == 0;
+  }
+  static __device__ __forceinline__ void store(const GemmArgs& a, uint64_t dst, uint32_t r, uint32_t j, float v) {
+    if (j < a.nb) a.y[j * a.ldy + dst + r] = v;
+  }
+  __device__ __forceinline__ void init() { acc = f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0,
+                                              uint32_t avail, bool final, const SmWin& W) {
+    const uint32_t take = final ? avail : (avail & ~255u);  // whole tiles for fitting streams
+    const uint32_t units = take >> 3, lu = lane_unit(lane), g = lane >> 4, n = lane & 15u;
+    const uint32_t t0 = (st.start + pos0) >> 8;  // slab tile of the call's first symbol
+    const uint16_t* xr = x + n * ldx;
+    for (uint32_t b = 0; 64 * b < units; ++b) {
+      const uint32_t u = 64 * b + lu;
+      const bool valid = u < units;  // an odd tile count leaves the last pair half empty
+      uint64_t E = 0, M = 0;
+      if (valid) {
+        __builtin_memcpy(&E, S.syms + 8 * u, 8);
+        M = b < 4 ? W.v[b] : ldg64(st.sm + pos0 + 8 * u);
+      }
+      const uint4 w = combine8(E, M);
+      uint4 xv = make_uint4(0u, 0u, 0u, 0u);
+      if (valid && n < nb) __builtin_memcpy(&xv, xr + 16u * (t0 + 2 * b + (g >> 1)) + 8u * (g & 1u), 16);
+      bf16x8 a, bb;
+      __builtin_memcpy(&a, &w, 16);
+      __builtin_memcpy(&bb, &xv, 16);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bb, acc, 0, 0, 0);
+    }
+    return take;
+  }
+  __device__ __forceinline__ void deposit(float* slots, uint32_t lane, uint32_t) {
+    const uint32_t r0 = 4u * (lane >> 4), n = lane & 15u;
+    slots[(r0 + 0) * 16 + n] += acc[0];
+    slots[(r0 + 1) * 16 + n] += acc[1];
+    slots[(r0 + 2) * 16 + n] += acc[2];
+    slots[(r0 + 3) * 16 + n] += acc[3];
   }
 };
 
@@ -1000,27 +1165,24 @@ k_decode_serial(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uin
   }
 }
 
-// Fused decode-GEMM for unit-aligned 16-row slabs, fp32 activations
-// X[c * ldx + j], output Y[(dst + r) * ldy + j].  One workgroup of W waves per
-// block: wave w takes substreams w, w + W, ... (prefetching each next one),
-// adds its per-row partial sums into its own LDS slots after every
-// substream, and the workgroup sums the W slots in wave order.  No atomics,
-// deterministic.
-template <int W, int NB>
-__global__ void __launch_bounds__(64 * W) k_gemm_f32(const DevBlock* __restrict__ blocks, uint32_t nblocks,
-                                                     uint32_t codec, const uint8_t* __restrict__ arc,
-                                                     const float* __restrict__ x, uint64_t ldx, uint32_t nb,
-                                                     float* __restrict__ y, uint64_t ldy,
-                                                     uint32_t* __restrict__ status) {
+// Fused decode-GEMM over 16-row slabs with consumer Acc (GemmF32, GemmBf16,
+// GemmMfma).  One workgroup of W waves per block: wave w takes substreams w,
+// w + W, ... (prefetching each next one), adds its partial sums into its own
+// LDS slots after every substream, and the workgroup sums the W slots in wave
+// order.  No atomics, deterministic.
+template <int W, class Acc>
+__global__ void __launch_bounds__(64 * W) k_gemm(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+                                                 uint32_t codec, const uint8_t* __restrict__ arc, GemmArgs ga,
+                                                 uint32_t* __restrict__ status) {
   __shared__ Smem SS[W];
-  __shared__ float red[W][16][NB];
+  __shared__ float red[W][Acc::kOut];
   __shared__ uint32_t werr[W];
   const uint32_t lane = lane_id(), w = threadIdx.x / 64;
   Smem& S = SS[w];
   for (uint32_t b = blockIdx.x; b < nblocks; b += gridDim.x) {
     const DevBlock d = blocks[b];
     const uint8_t* blk = arc + d.src;
-    for (uint32_t i = lane; i < 16 * NB; i += kWave) red[w][i / NB][i % NB] = 0.f;
+    for (uint32_t i = lane; i < (uint32_t)Acc::kOut; i += kWave) red[w][i] = 0.f;
     uint32_t err = 0, chunks = 1;
     uint64_t hv = 0;
     if (codec == kCodecParallel) {
@@ -1040,7 +1202,8 @@ __global__ void __launch_bounds__(64 * W) k_gemm_f32(const DevBlock* __restrict_
         len = k < chunks ? rdlane64(hv, 4 + k) : 0;
       }
       StreamIn P, PN;
-      if (k < chunks) issue_stream(P, blk + off, blk + off + len, (uint32_t)(total * (k + 1) / chunks - total * k / chunks), lane);
+      if (k < chunks)
+        issue_stream(P, blk + off, blk + off + len, (uint32_t)(total * (k + 1) / chunks - total * k / chunks), lane);
       for (; k < chunks && !err; k += W) {
         const uint32_t s0 = (uint32_t)(total * k / chunks), s1 = (uint32_t)(total * (k + 1) / chunks);
         // next substream of this wave
@@ -1051,20 +1214,15 @@ __global__ void __launch_bounds__(64 * W) k_gemm_f32(const DevBlock* __restrict_
           nlen = rdlane64(hv, 4 + kn);
         }
         const uint32_t ncount = kn < chunks ? (uint32_t)(total * (kn + 1) / chunks - total * kn / chunks) : 0u;
-        if (!unit_aligned(s0, s1 - s0, d.rows, d.cols)) {
+        if (!Acc::fits(s0, s1 - s0, d.rows, d.cols)) {
           err = kErrShape;
           break;
         }
-        GemmF32<NB> C{x, ldx, nb, {}};
+        Acc C(ga);
         C.init();
         err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, P, C, kn < chunks ? blk + noff : nullptr,
                          blk + noff + nlen, ncount, PN);
-        const uint32_t su = (s0 >> 3) & 1u;
-        C.reduce(lane, su);
-        const uint32_t row = (((s0 >> 3) + lane) >> 1) & 15u;
-        if (lane < 32 && ((lane + su) & 1u) == 0)
-#pragma unroll
-          for (int j = 0; j < NB; ++j) red[w][row][j] += C.acc[j];
+        C.deposit(red[w], lane, s0);
         P = PN;
         off = noff;
         len = nlen;
@@ -1077,12 +1235,11 @@ __global__ void __launch_bounds__(64 * W) k_gemm_f32(const DevBlock* __restrict_
     if (w == 0) {
       set_status(status, d.status_slot, any, lane);
       if (!any)
-        for (uint32_t i = lane; i < 16 * NB; i += kWave) {
-          const uint32_t r = i / NB, j = i % NB;
-          float s = 0.f;
+        for (uint32_t i = lane; i < (uint32_t)Acc::kOut; i += kWave) {
+          float sum = 0.f;
 #pragma unroll
-          for (int q = 0; q < W; ++q) s += red[q][r][j];
-          if (j < nb) y[(d.dst + r) * ldy + j] = s;
+          for (int q = 0; q < W; ++q) sum += red[q][i];
+          Acc::store(ga, d.dst, i / Acc::kCols, i % Acc::kCols, sum);
         }
     }
     __syncthreads();
@@ -1140,6 +1297,38 @@ __global__ void __launch_bounds__(64) k_gemm_plain(const DevBlock* __restrict__ 
   }
 }
 
+// The same over bf16 activations in the layout of x @ W.T:
+// Y[j * ldy + dst + r] = sum_c W[r, c] X[j * ldx + c].
+__global__ void __launch_bounds__(64) k_gemm_plain_bf16(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+                                                        const uint8_t* __restrict__ base,
+                                                        const uint16_t* __restrict__ x, uint64_t ldx, uint32_t nb,
+                                                        float* __restrict__ y, uint64_t ldy) {
+  const uint32_t lane = lane_id();
+  for (uint32_t b = blockIdx.y; b < nblocks; b += gridDim.y) {
+    const DevBlock d = blocks[b];
+    for (uint64_t r = blockIdx.x; r < d.rows; r += gridDim.x) {
+      const uint8_t* wrow = base + d.src + r * d.cols * 2;
+      for (uint32_t j0 = 0; j0 < nb; j0 += 4) {
+        float a[4] = {0.f, 0.f, 0.f, 0.f};
+        for (uint64_t c = lane; c < d.cols; c += kWave) {
+          uint16_t h;
+          __builtin_memcpy(&h, wrow + 2 * c, 2);
+          const float wv = __uint_as_float((uint32_t)h << 16);
+#pragma unroll
+          for (uint32_t j = 0; j < 4; ++j)
+            if (j0 + j < nb) a[j] = fmaf(wv, __uint_as_float((uint32_t)x[(j0 + j) * ldx + c] << 16), a[j]);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+#pragma unroll
+          for (uint32_t dd = kWave / 2; dd >= 1; dd >>= 1) a[j] += __shfl_xor(a[j], dd, kWave);
+          if (lane == 0 && j0 + j < nb) y[(j0 + j) * ldy + d.dst + r] = a[j];
+        }
+      }
+    }
+  }
+}
+
 __global__ void k_fill_u32(uint32_t* p, uint64_t n, uint32_t v) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
     p[i] = v;
@@ -1179,33 +1368,54 @@ hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t code
   return hipGetLastError();
 }
 
-template <int W, int NB>
-static void gemm_f32_launch(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec,
-                            const uint8_t* arc, const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy,
-                            uint32_t* status, unsigned cus) {
-  static const unsigned per_cu = groups_per_cu(k_gemm_f32<W, NB>, 64 * W);
-  hipLaunchKernelGGL((k_gemm_f32<W, NB>), dim3(grid_for(nblocks, per_cu * cus)), dim3(64 * W), 0, s, blocks, nblocks, codec,
-                     arc, x, ldx, nb, y, ldy, status);
+template <int W, class Acc>
+static void gemm_launch(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
+                        const GemmArgs& ga, uint32_t* status, unsigned cus) {
+  static const unsigned per_cu = groups_per_cu(k_gemm<W, Acc>, 64 * W);
+  hipLaunchKernelGGL((k_gemm<W, Acc>), dim3(grid_for(nblocks, per_cu * cus)), dim3(64 * W), 0, s, blocks, nblocks,
+                     codec, arc, ga, status);
 }
 
-template <int W>
-static void gemm_f32_w(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
-                       const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
-                       unsigned cus) {
-  if (nb == 1) gemm_f32_launch<W, 1>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
-  else if (nb <= 4) gemm_f32_launch<W, 4>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
-  else if (nb <= 8) gemm_f32_launch<W, 8>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
-  else gemm_f32_launch<W, 16>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
+// Parallel32 blocks run one workgroup of 4 waves per block (substreams split
+// over the waves), serial blocks one wave per block.
+template <template <int> class Acc>
+static void gemm_valu(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
+                      const GemmArgs& ga, uint32_t* status, unsigned cus) {
+  const bool par = codec == kCodecParallel;
+  if (ga.nb == 1) {
+    if (par) gemm_launch<4, Acc<1>>(s, blocks, nblocks, codec, arc, ga, status, cus);
+    else gemm_launch<1, Acc<1>>(s, blocks, nblocks, codec, arc, ga, status, cus);
+  } else if (ga.nb <= 4) {
+    if (par) gemm_launch<4, Acc<4>>(s, blocks, nblocks, codec, arc, ga, status, cus);
+    else gemm_launch<1, Acc<4>>(s, blocks, nblocks, codec, arc, ga, status, cus);
+  } else if (ga.nb <= 8) {
+    if (par) gemm_launch<4, Acc<8>>(s, blocks, nblocks, codec, arc, ga, status, cus);
+    else gemm_launch<1, Acc<8>>(s, blocks, nblocks, codec, arc, ga, status, cus);
+  } else {
+    if (par) gemm_launch<4, Acc<16>>(s, blocks, nblocks, codec, arc, ga, status, cus);
+    else gemm_launch<1, Acc<16>>(s, blocks, nblocks, codec, arc, ga, status, cus);
+  }
 }
 
 hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
-                           float*, uint32_t*, unsigned cus, hipStream_t s) {
+                           unsigned cus, hipStream_t s) {
   if (!nblocks) return hipSuccess;
-  if (codec == kCodecParallel)
-    gemm_f32_w<4>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
-  else
-    gemm_f32_w<1>(s, blocks, nblocks, codec, arc, x, ldx, nb, y, ldy, status, cus);
+  gemm_valu<GemmF32>(s, blocks, nblocks, codec, arc, GemmArgs{x, ldx, nb, y, ldy}, status, cus);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_bf16(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
+                            const uint16_t* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, bool mfma,
+                            uint32_t* status, unsigned cus, hipStream_t s) {
+  if (!nblocks) return hipSuccess;
+  const GemmArgs ga{x, ldx, nb, y, ldy};
+  if (mfma && nb >= 8) {
+    if (codec == kCodecParallel) gemm_launch<4, GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, cus);
+    else gemm_launch<1, GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, cus);
+  } else {
+    gemm_valu<GemmBf16>(s, blocks, nblocks, codec, arc, ga, status, cus);
+  }
   return hipGetLastError();
 }
 
@@ -1221,6 +1431,14 @@ hipError_t launch_gemm_plain(const DevBlock* blocks, uint32_t nblocks, const uin
   if (!nblocks) return hipSuccess;
   hipLaunchKernelGGL(k_gemm_plain, dim3(256, nblocks < 256 ? nblocks : 256), dim3(64), 0, s, blocks, nblocks, base, x,
                      ldx, nb, y, ldy);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_plain_bf16(const DevBlock* blocks, uint32_t nblocks, const uint8_t* base, const uint16_t* x,
+                                  uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, hipStream_t s) {
+  if (!nblocks) return hipSuccess;
+  hipLaunchKernelGGL(k_gemm_plain_bf16, dim3(256, nblocks < 256 ? nblocks : 256), dim3(64), 0, s, blocks, nblocks,
+                     base, x, ldx, nb, y, ldy);
   return hipGetLastError();
 }
 

@@ -36,8 +36,7 @@ struct DevBlock {
 
 // Device element limit per block: element indices are 32-bit in the kernels.
 constexpr uint64_t kMaxBlockElems = (1ull << 31) - 1;
-// Partial-sum slots per parallel block for the deterministic cross-substream
-// reduction of the fused GEMV (one per substream).
+// Most substreams an XKSP2 block may hold (src/c_api.cpp:66-72).
 constexpr uint32_t kMaxChunks = 32;
 // Largest batch one fused GEMM launch handles in registers; larger batches
 // are split into column groups by the host.

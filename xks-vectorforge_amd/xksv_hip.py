@@ -52,6 +52,7 @@ _SIGNATURES = {
     "xksv_hip_decode_parallel": (_int, [_vp, _sz, _vp]),
     "xksv_hip_gemv_parallel": (_int, [_vp, _sz, _vp, _vp]),
     "xksv_hip_gemm_parallel": (_int, [_vp, _sz, _sz, _vp, _vp]),
+    "xksv_hip_gemm_parallel_bf16": (_int, [_vp, _sz, _sz, _vp, _vp]),
     "xksv_cuda_decode": (_int, [_vp, _sz, _sz, _sz, _vp]),
     "xksv_cuda_gemv": (_int, [_vp, _sz, _sz, _sz, _vp, _vp]),
     "xksv_cuda_gemm": (_int, [_vp, _sz, _sz, _sz, _sz, _vp, _vp]),
@@ -61,6 +62,7 @@ _SIGNATURES = {
     "xksv_hip_plan_destroy": (_int, [_vp]),
     "xksv_hip_plan_decode": (_int, [_vp, _vp, _vp, _u64, _vp]),
     "xksv_hip_plan_gemm": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
+    "xksv_hip_plan_gemm_bf16": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "xksv_hip_plan_errors": (ctypes.c_int64, [_vp, _vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(_u32)]),
     "xksv_encode_tensor": (_int, [_vp, _u64, _int, _u64, _u32, _u32, _pvp, ctypes.POINTER(_u64),
                                   ctypes.POINTER(ctypes.POINTER(Block)), ctypes.POINTER(_u64)]),
@@ -148,6 +150,11 @@ class Library:
         return self.lib.xksv_hip_gemm_parallel(ctypes.create_string_buffer(bytes(block), max(len(block), 1)),
                                                len(block), batch, x_ptr, y_ptr)
 
+    def gemm_parallel_bf16(self, block: bytes, batch: int, x_ptr: int, y_ptr: int) -> int:
+        """bf16 X [batch, cols] -> fp32 Y [batch, rows] (layout of x @ W.T)."""
+        return self.lib.xksv_hip_gemm_parallel_bf16(ctypes.create_string_buffer(bytes(block), max(len(block), 1)),
+                                                    len(block), batch, x_ptr, y_ptr)
+
     # -- whole-tensor encoder (compile step) --
     def encode_tensor(self, words: np.ndarray, codec: int, shape_cols: int | None = None, bf16: bool = True,
                       threads: int = 0):
@@ -198,6 +205,11 @@ class Plan:
     def gemm(self, archive_ptr: int, x_ptr: int, batch: int, y_ptr: int, stream: int = 0) -> None:
         if self.lib.lib.xksv_hip_plan_gemm(self.handle, archive_ptr, x_ptr, batch, y_ptr, stream or None):
             raise XksvError("xksv_hip_plan_gemm failed to launch")
+
+    def gemm_bf16(self, archive_ptr: int, x_ptr: int, batch: int, y_ptr: int, stream: int = 0) -> None:
+        """bf16 X [batch, cols] -> fp32 Y [batch, M] (layout of x @ W.T)."""
+        if self.lib.lib.xksv_hip_plan_gemm_bf16(self.handle, archive_ptr, x_ptr, batch, y_ptr, stream or None):
+            raise XksvError("xksv_hip_plan_gemm_bf16 failed to launch")
 
     def errors(self, stream: int = 0):
         """(number of failed blocks, first failing block or -1, OR of error bits)."""
