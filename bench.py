@@ -146,6 +146,90 @@ def gemv_bench(torch, lib, rows: int, cols: int, copies: int, steps: int, warmup
             "errors": int(nbad), "copies": copies}
 
 
+def gemm_bf16_bench(torch, lib, rows: int, cols: int, batches, copies: int, steps: int, warmup: int, stream) -> dict:
+    """Fused decode-GEMM with bf16 X [batch, cols] (bf16 MFMA from batch 8) over `copies` resident
+    copies of one parallel32 layer; rel-L2 against an fp64 GEMM of the same bf16 values."""
+    import xksv_hip
+    w = gen_bf16(torch, (rows, cols), 91 + rows, False)
+    words = w.view(torch.int16).cpu().numpy().view(np.uint16)
+    enc, table = lib.encode_tensor(words, 2)
+    table = table.copy()
+    table["out_offset"] //= cols * 2
+    arcs = [torch.from_numpy(enc).to("cuda") for _ in range(copies)]
+    plan = xksv_hip.Plan(lib, table, enc.nbytes)
+    s = stream.cuda_stream
+    out = {}
+    for batch in batches:
+        x = torch.randn(batch, cols, device="cuda").to(torch.bfloat16)
+        y = torch.empty(batch, rows, device="cuda", dtype=torch.float32)
+        it = [0]
+
+        def step():
+            plan.gemm_bf16(arcs[it[0] % copies].data_ptr(), x.data_ptr(), batch, y.data_ptr(), s)
+            it[0] += 1
+
+        for _ in range(max(warmup, 1) * copies):
+            step()
+        nbad = plan.errors(s)[0]
+        ref = x.double() @ w.double().T
+        rel = (torch.linalg.norm(y.double() - ref) / torch.linalg.norm(ref)).item()
+        ms = time_events(torch, step, steps * copies, stream)
+        alg = enc.nbytes + batch * cols * 2 + batch * rows * 4
+        out[str(batch)] = {"us_per_layer": round(ms * 1e3, 2), "gbps": round(alg / (ms * 1e-3) / 1e9, 1),
+                           "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "rel_l2_vs_fp64": rel,
+                           "mfma": batch >= 8, "errors": int(nbad)}
+        del ref
+    plan.close()
+    return {"encoded_bytes": int(enc.nbytes), "copies": copies, "batches": out}
+
+
+def small_archive_bench(torch, lib, tensors, codec: int, steps: int, warmup: int, stream) -> dict:
+    """Decode GB/s of a small archive (repeated steps; it fits in the last-level cache, so this is
+    a parity-and-throughput report, not a roofline figure) plus a bit-exact check."""
+    import xksv_hip
+    encs, tables, words_all = [], [], []
+    arc_off = out_off = 0
+    for shape, kind, seed in tensors:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        if kind == "normal":
+            t = (torch.randn(shape, generator=g, device="cuda") * 0.02).to(torch.bfloat16).view(torch.int16)
+        elif kind == "student_t":
+            z = torch.randn(shape, generator=g, device="cuda")
+            v = sum(torch.randn(shape, generator=g, device="cuda") ** 2 for _ in range(3)) / 3.0
+            t = (z / v.sqrt() * 0.02).to(torch.bfloat16).view(torch.int16)
+        elif kind == "uniform":
+            t = (torch.rand(shape, generator=g, device="cuda") * 2 - 1).to(torch.bfloat16).view(torch.int16)
+        elif kind == "zeros":
+            t = torch.zeros(shape, device="cuda", dtype=torch.int16)
+        else:  # fp32 vector, left raw
+            t = torch.randn(shape, generator=g, device="cuda").view(torch.int16)
+        words = t.cpu().numpy().view(np.uint16)
+        enc, table = lib.encode_tensor(words, codec, bf16=kind != "fp32")
+        table = table.copy()
+        table["offset"] += arc_off
+        table["out_offset"] += out_off
+        encs.append(enc)
+        tables.append(table)
+        words_all.append(words.reshape(-1))
+        arc_off += enc.nbytes
+        out_off += words.nbytes
+    table = np.concatenate(tables)
+    d_arc = torch.from_numpy(np.concatenate(encs)).to("cuda")
+    d_out = torch.empty(out_off, dtype=torch.uint8, device="cuda")
+    plan = xksv_hip.Plan(lib, table, d_arc.numel())
+    s = stream.cuda_stream
+    for _ in range(max(1, warmup)):
+        plan.decode(d_arc.data_ptr(), d_out.data_ptr(), out_off, s)
+    nbad = plan.errors(s)[0]
+    want = torch.from_numpy(np.concatenate(words_all).view(np.uint8)).to("cuda")
+    exact = nbad == 0 and torch.equal(d_out, want)
+    ms = time_events(torch, lambda: plan.decode(d_arc.data_ptr(), d_out.data_ptr(), out_off, s), steps, stream)
+    plan.close()
+    return {"blocks": int(len(table)), "encoded_bytes": int(d_arc.numel()), "decoded_bytes": int(out_off),
+            "ms": round(ms, 4), "decoded_gbps": round(out_off / (ms * 1e-3) / 1e9, 1), "bit_exact": bool(exact)}
+
+
 def copy_bench(torch, steps: int, stream) -> float:
     n = 1 << 31
     a = torch.empty(n, dtype=torch.uint8, device="cuda")
@@ -196,7 +280,8 @@ def main() -> int:
     ap.add_argument("--cpu-slabs", type=int, default=0,
                     help="parallel32 blocks in the CPU-baseline sample (0 = every block of the archive)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "decode", "gemv", "copy"], default="all",
+    ap.add_argument("--gemm-copies", type=int, default=4)
+    ap.add_argument("--only", choices=["all", "decode", "gemv", "gemm", "copy"], default="all",
                     help="run one part only (for profiler runs); prints no result line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -217,6 +302,12 @@ def main() -> int:
         for rows, cols in ((14336, 4096), (4096, 14336)):
             g = gemv_bench(torch, lib, rows, cols, args.gemv_copies, args.steps, args.warmup, stream)
             log(f"gemv {rows}x{cols} {g['us_per_layer']} us, rel-L2 {g['rel_l2_vs_fp64']:.2e}")
+        return 0
+    if args.only == "gemm":
+        for rows, cols in ((28672, 8192), (8192, 28672)):
+            g = gemm_bf16_bench(torch, lib, rows, cols, (1, 4, 8, 16), args.gemm_copies, args.steps, args.warmup,
+                                stream)
+            log(f"gemm bf16 {rows}x{cols}: " + ", ".join(f"b{b} {v['us_per_layer']} us" for b, v in g["batches"].items()))
         return 0
     if args.only == "copy":
         log(f"copy {copy_bench(torch, args.steps, stream):.1f} GB/s (2 GiB read + 2 GiB written per step)")
@@ -247,6 +338,17 @@ def main() -> int:
     g1 = gemv_bench(torch, lib, 14336, 4096, args.gemv_copies, args.steps, args.warmup, stream)
     g2 = gemv_bench(torch, lib, 4096, 14336, args.gemv_copies, args.steps, args.warmup, stream)
     log(f"gemv 14336x4096 {g1['us_per_layer']} us, 4096x14336 {g2['us_per_layer']} us")
+    g5 = {f"{r}x{c}": gemm_bf16_bench(torch, lib, r, c, (1, 4, 8, 16), args.gemm_copies, args.steps, args.warmup,
+                                      stream) for r, c in ((28672, 8192), (8192, 28672))}
+    log("gemm bf16 " + "; ".join(f"{k}: " + ", ".join(f"b{b} {v['us_per_layer']} us" for b, v in g["batches"].items())
+                                 for k, g in g5.items()))
+    c1 = small_archive_bench(torch, lib, [((4096, 4096), "normal", 0)], 1, args.steps, args.warmup, stream)
+    mixed = [((4096, 4096), "normal", 1), ((4096, 4096), "student_t", 2), ((4096, 4096), "uniform", 3),
+             ((4096, 4096), "zeros", 4), ((4096,), "fp32", 5)]
+    c3 = {"serial": small_archive_bench(torch, lib, mixed, 1, args.steps, args.warmup, stream),
+          "parallel": small_archive_bench(torch, lib, mixed, 2, args.steps, args.warmup, stream)}
+    log(f"4096x4096 serial {c1['decoded_gbps']} GB/s exact={c1['bit_exact']}; mixed serial "
+        f"{c3['serial']['decoded_gbps']} / parallel {c3['parallel']['decoded_gbps']} GB/s")
     copy_gbps = copy_bench(torch, 10, stream)
 
     traffic = None
@@ -274,6 +376,8 @@ def main() -> int:
         "hbm_pct_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "gemv_us_per_layer_14336x4096": g1["us_per_layer"],
         "gemv_14336x4096": g1, "gemv_4096x14336": g2,
+        "gemm_bf16_70b": g5,
+        "decode_4096x4096_serial": c1, "decode_mixed_archive": c3,
         "hbm_copy_gbps": round(copy_gbps, 1),
     }
     print(json.dumps(line), flush=True)
