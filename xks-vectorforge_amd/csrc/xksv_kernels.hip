@@ -156,19 +156,27 @@ __device__ __forceinline__ uint32_t ldg32(const uint8_t* p) {
   __builtin_memcpy(&v, p, 4);
   return v;
 }
-// 16 bytes at p; bytes at or past `end` read as zero and are never fetched.
+// 16 bytes at p; bytes at or past `end` read as zero.  One 16-byte load that
+// never crosses `end`: near the end it reads the 16 bytes before `end` and
+// shifts.  Callers guarantee [end - 16, end) is inside the same buffer (every
+// segment holds at least 272 header bytes before its code bytes).
 __device__ __forceinline__ uint4 ldg16_bounded(const uint8_t* p, const uint8_t* end) {
+  if (p >= end) return make_uint4(0u, 0u, 0u, 0u);
+  const uint8_t* q = p + 16 <= end ? p : end - 16;
   uint4 v;
-  if (p + 16 <= end) {
-    __builtin_memcpy(&v, p, 16);
-    return v;
-  }
-  uint32_t w[4] = {0, 0, 0, 0};
+  __builtin_memcpy(&v, q, 16);
+  const uint32_t sh = (uint32_t)(p - q), d = sh >> 2, r = sh & 3u;  // drop the first sh bytes
+  const uint32_t w[5] = {v.x, v.y, v.z, v.w, 0u};
+  uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    if (p + i < end) w[i >> 2] |= (uint32_t)p[i] << (8 * (i & 3));
-  v.x = w[0]; v.y = w[1]; v.z = w[2]; v.w = w[3];
-  return v;
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t lo = d == 0 ? w[k] : d == 1 ? w[k + 1 < 5 ? k + 1 : 4] : d == 2 ? w[k + 2 < 5 ? k + 2 : 4]
+                                                                                    : w[k + 3 < 5 ? k + 3 : 4];
+    const uint32_t hi = d == 0 ? w[k + 1 < 5 ? k + 1 : 4] : d == 1 ? w[k + 2 < 5 ? k + 2 : 4]
+                                                                    : d == 2 ? w[k + 3 < 5 ? k + 3 : 4] : 0u;
+    o[k] = r ? __builtin_amdgcn_alignbyte(hi, lo, r) : lo;
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
 }
 __device__ __forceinline__ uint32_t lds32(const uint8_t* p) {
   uint32_t v;
@@ -538,6 +546,24 @@ __device__ __forceinline__ void issue_sm(SmWin& W, const uint8_t* sm, uint32_t p
     W.v[i] = p + 8 <= count ? ldg64(sm + p) : 0ull;
   }
 }
+// The stream after the current one (seg == nullptr: none); its inputs are
+// issued when the current stream starts and land while it decodes.
+struct NextStream {
+  const uint8_t* seg;
+  const uint8_t* end;
+  uint32_t count;
+  __device__ __forceinline__ void issue(StreamIn& PN, uint32_t lane) const {
+    if (seg) issue_stream(PN, seg, end, count, lane);
+  }
+};
+
+// Wait for every outstanding global load (and store).  Called just before a
+// consumer issues its stores, when all that is in flight is prefetches issued
+// long before: on this architecture loads and stores share one in-order
+// counter, so a later wait for those prefetches would also wait for the
+// consumer's fresh stores.
+__device__ __forceinline__ void drain_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0) only
+
 __device__ __forceinline__ void stage_bits(Smem& S, uint32_t lane, uint4 v) {
   if (lane < kStreamLanes) {
     uint32_t* w = &S.stream[1 + 4 * lane];
@@ -548,23 +574,39 @@ __device__ __forceinline__ void stage_bits(Smem& S, uint32_t lane, uint4 v) {
   }
 }
 
+// Hand a stream's prefetched inputs to LDS: its first 784 code bytes into the
+// segment buffer (behind a zero dword), its 256 code lengths into `sorted`
+// (read back before the tables are built) and its header words into `bcast`.
+// Called where every load is known to have landed -- right after
+// drain_loads() -- so the next stream starts without waiting on the memory
+// counter, which by then also counts this stream's output stores.
+__device__ __forceinline__ void stage_inputs(Smem& S, uint32_t lane, const StreamIn& P) {
+  stage_bits(S, lane, P.bits);
+  if (lane == 0) S.stream[0] = 0;
+  reinterpret_cast<uint32_t*>(S.sorted)[lane] = P.lens;
+  if (lane < 2) reinterpret_cast<uint64_t*>(S.bcast)[lane] = P.hdr;
+  wave_sync();
+}
+
 // Decode one stream with the fast tables; the consumer receives the
 // exponents in stream order.  `first` holds the stream's first 784 code
 // bytes; later segments are loaded one segment ahead.  Returns error bits.
 template <class Cons>
-__device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen, const uint8_t* blk_end,
-                                const uint4 first, Cons& C) {
+__device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen,
+                                                const uint8_t* blk_end, Cons& C, const StreamIn& PN, bool next) {
   const uint64_t nbits = st.nbits;
   const uint8_t* bend = st.bits + ((nbits + 7) >> 3);
   if (bend > blk_end) bend = blk_end;
   uint8_t* const region = S.syms + kCarry + lane * kRegion;
   uint32_t carry = 0, pos0 = 0, entry = 0, err = 0;
   uint64_t S0 = 0, true_pos = 0;
-  uint4 cur = first;
-  if (lane == 0) S.stream[0] = 0;
+  uint4 cur = make_uint4(0u, 0u, 0u, 0u);
+  bool staged = false;
   while (true_pos < nbits) {
-    stage_bits(S, lane, cur);
-    wave_sync();
+    if (S0) {  // the first segment's bytes were staged with the stream's inputs
+      stage_bits(S, lane, cur);
+      wave_sync();
+    }
     // Next segment's code bytes and this segment's sign/mantissa window go
     // out now and land while the segment decodes.
     if (S0 + kSegBits < nbits && lane < kStreamLanes)
@@ -654,6 +696,11 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
     }
     const uint32_t avail = carry + total;
     const bool fin = S0 + seg_exit >= nbits;  // last segment: hand over everything
+    drain_loads();
+    if (fin && next) {  // this stream is done with the segment buffer
+      stage_inputs(S, lane, PN);
+      staged = true;
+    }
     const uint32_t take = C.consume(S, lane, st, pos0, avail, fin, W);
     const uint32_t rem = avail - take;
     if (take && rem) {  // take is a multiple of 256 here, so source and destination do not overlap
@@ -670,6 +717,10 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
   }
   if (!err && (true_pos != nbits || (uint64_t)pos0 + carry != st.count)) err = kErrStream;
   wave_sync();
+  if (next && !staged) {  // left early (an error): hand the next stream's inputs on anyway
+    drain_loads();
+    stage_inputs(S, lane, PN);
+  }
   return err;
 }
 
@@ -677,7 +728,8 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
 // the code one bit at a time (d = offset from the first code of the current
 // length); the consumer sees the symbols kSlowSeg at a time.
 template <class Cons>
-__device__ __forceinline__ uint32_t decode_slow(Smem& S, uint32_t lane, const Stream& st, Cons& C) {
+__device__ __forceinline__ uint32_t decode_slow(Smem& S, uint32_t lane, const Stream& st, Cons& C,
+                                                const StreamIn& PN, bool next) {
   const SlowTables& T = S.t.s;
   const uint64_t nbits = st.nbits;
   uint64_t pos = 0;
@@ -715,6 +767,7 @@ __device__ __forceinline__ uint32_t decode_slow(Smem& S, uint32_t lane, const St
     if (err) break;
     SmWin W;
     issue_sm(W, st.sm, produced, st.count, Cons::lane_unit(lane));
+    drain_loads();
     C.consume(S, lane, st, produced, nseg, produced + nseg == st.count, W);
     wave_sync();
     produced += nseg;
@@ -723,20 +776,37 @@ __device__ __forceinline__ uint32_t decode_slow(Smem& S, uint32_t lane, const St
   wave_sync();
   if (!err && !S.bcast[1]) err = kErrStream;
   wave_sync();
+  if (next) {  // after the last use of bcast (this path is rare: codes over 32 bits)
+    drain_loads();
+    stage_inputs(S, lane, PN);
+  }
   return err;
 }
 
-// One stream from prefetched inputs P.  Before any work, the next stream's
-// inputs are issued into PN (when `nseg` is given) so they load while this
-// stream decodes.
+// A stream that fails before decoding still hands the next stream's inputs on.
+__device__ __forceinline__ uint32_t fail_stream(Smem& S, uint32_t lane, uint32_t err, const NextStream& N,
+                                                const StreamIn& PN) {
+  if (N.seg) {
+    drain_loads();
+    stage_inputs(S, lane, PN);
+  }
+  return err;
+}
+
+// Header checks [src/c_api.cpp:29-40, cuda/decode.cu:47-51], tables, decode.
+// The next stream's inputs are issued once this stream's header and lengths
+// are in use: loads complete in issue order, so a wait for them issued after
+// the prefetch would wait for the prefetch too.
 template <class Cons>
-__device__ __forceinline__ uint32_t run_stream(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end, uint32_t count,
-                               uint32_t start, const StreamIn& P, Cons& C, const uint8_t* nseg,
-                               const uint8_t* nseg_end, uint32_t ncount, StreamIn& PN) {
-  if (nseg) issue_stream(PN, nseg, nseg_end, ncount, lane);
+__device__ __forceinline__ uint32_t stream_body(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end,
+                                                uint32_t count, uint32_t start, Cons& C, const NextStream& N,
+                                                StreamIn& PN) {
   const uint64_t len = (uint64_t)(seg_end - seg);
-  const uint64_t cnt = rdlane64(P.hdr, 0), nb = rdlane64(P.hdr, 1);
-  if (cnt != count || cnt > len - 272 || nb / 8 + (nb % 8 != 0) != len - 272 - cnt) return kErrHeader;
+  const uint64_t cnt = reinterpret_cast<const uint64_t*>(S.bcast)[0], nb = reinterpret_cast<const uint64_t*>(S.bcast)[1];
+  const uint32_t lw = reinterpret_cast<const uint32_t*>(S.sorted)[lane];
+  wave_sync();  // the staged inputs are read before the tables overwrite them
+  N.issue(PN, lane);
+  if (cnt != count || cnt > len - 272 || nb / 8 + (nb % 8 != 0) != len - 272 - cnt) return fail_stream(S, lane, kErrHeader, N, PN);
   Stream st;
   st.lengths = seg + 16;
   st.sm = seg + 272;
@@ -744,9 +814,22 @@ __device__ __forceinline__ uint32_t run_stream(Smem& S, uint32_t lane, const uin
   st.nbits = nb;
   st.count = count;
   st.start = start;
-  const Book b = build_book(S, lane, P.lens);
-  if (b.err) return b.err;
-  return b.fast ? decode_fast(S, lane, st, b.maxlen, seg_end, P.bits, C) : decode_slow(S, lane, st, C);
+  const Book b = build_book(S, lane, lw);
+  if (b.err) return fail_stream(S, lane, b.err, N, PN);
+  const uint32_t err =
+      b.fast ? decode_fast(S, lane, st, b.maxlen, seg_end, C, PN, N.seg) : decode_slow(S, lane, st, C, PN, N.seg);
+  return err;
+}
+
+// One stream whose inputs were staged in LDS (stage_inputs); the next
+// stream's inputs are issued into PN (when N.seg is given) early on, so they
+// load while this stream decodes, and staged when it finishes.  A stream that
+// fails before its last segment stages them on the way out.
+template <class Cons>
+__device__ __forceinline__ uint32_t run_stream(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end,
+                                               uint32_t count, uint32_t start, Cons& C, const NextStream& N,
+                                               StreamIn& PN) {
+  return stream_body(S, lane, seg, seg_end, count, start, C, N, PN);
 }
 
 // ------------------------------------------------------------- consumers
@@ -932,19 +1015,20 @@ struct GemmBf16 {
                         bf_lo(w.z), bf_hi(w.z), bf_lo(w.w), bf_hi(w.w)};
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      if (j >= (int)nb) break;
-      uint4 xv;
-      __builtin_memcpy(&xv, x + j * ldx + col, 16);
-      float a = acc[j];
-      a = fmaf(f[0], bf_lo(xv.x), a);
-      a = fmaf(f[1], bf_hi(xv.x), a);
-      a = fmaf(f[2], bf_lo(xv.y), a);
-      a = fmaf(f[3], bf_hi(xv.y), a);
-      a = fmaf(f[4], bf_lo(xv.z), a);
-      a = fmaf(f[5], bf_hi(xv.z), a);
-      a = fmaf(f[6], bf_lo(xv.w), a);
-      a = fmaf(f[7], bf_hi(xv.w), a);
-      acc[j] = a;
+      if (j < (int)nb) {
+        uint4 xv;
+        __builtin_memcpy(&xv, x + j * ldx + col, 16);
+        float a = acc[j];
+        a = fmaf(f[0], bf_lo(xv.x), a);
+        a = fmaf(f[1], bf_hi(xv.x), a);
+        a = fmaf(f[2], bf_lo(xv.y), a);
+        a = fmaf(f[3], bf_hi(xv.y), a);
+        a = fmaf(f[4], bf_lo(xv.z), a);
+        a = fmaf(f[5], bf_hi(xv.z), a);
+        a = fmaf(f[6], bf_lo(xv.w), a);
+        a = fmaf(f[7], bf_hi(xv.w), a);
+        acc[j] = a;
+      }
     }
   }
   __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0,
@@ -1114,17 +1198,18 @@ k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
     Writer C{out + d.dst, d.rows, d.cols, (uint32_t)(d.cols / 16), false};
     uint64_t off = 32 + 8ull * chunks;
     uint64_t len = rdlane64(seglen_v, 4);
-    StreamIn P, PN;
-    issue_stream(P, blk + off, blk + off + len, (uint32_t)(total / chunks), lane);
+    StreamIn PN;
+    issue_stream(PN, blk + off, blk + off + len, (uint32_t)(total / chunks), lane);
+    drain_loads();
+    stage_inputs(S, lane, PN);
     for (uint32_t k = 0; k < chunks && !err; ++k) {
       const uint32_t s0 = (uint32_t)(total * k / chunks), s1 = (uint32_t)(total * (k + 1) / chunks);
       const uint64_t noff = off + len;
       const uint64_t nlen = k + 1 < chunks ? rdlane64(seglen_v, 4 + k + 1) : 0ull;
       const uint32_t ncount = k + 1 < chunks ? (uint32_t)(total * (k + 2) / chunks) - s1 : 0u;
       C.aligned = aligned && unit_aligned(s0, s1 - s0, d.rows, d.cols);
-      err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, P, C,
-                       k + 1 < chunks ? blk + noff : nullptr, blk + noff + nlen, ncount, PN);
-      P = PN;
+      err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, C,
+                       NextStream{k + 1 < chunks ? blk + noff : nullptr, blk + noff + nlen, ncount}, PN);
       off = noff;
       len = nlen;
     }
@@ -1139,11 +1224,14 @@ k_decode_serial(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uin
                 uint8_t* __restrict__ out, uint32_t* __restrict__ status, uint32_t* queue) {
   __shared__ Smem S;
   const uint32_t lane = lane_id();
-  StreamIn P, PN;
+  StreamIn PN;
   uint32_t b = blockIdx.x;
-  if (b < nblocks && blocks[b].size >= 272)
-    issue_stream(P, arc + blocks[b].src, arc + blocks[b].src + blocks[b].size,
+  if (b < nblocks && blocks[b].size >= 272) {
+    issue_stream(PN, arc + blocks[b].src, arc + blocks[b].src + blocks[b].size,
                  (uint32_t)(blocks[b].rows * blocks[b].cols), lane);
+    drain_loads();
+    stage_inputs(S, lane, PN);
+  }
   for (uint32_t bn; b < nblocks; b = bn) {
     const DevBlock d = blocks[b];
     bn = claim_next(queue, b, lane);
@@ -1155,12 +1243,15 @@ k_decode_serial(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uin
     if (!err) {
       const uint32_t n = (uint32_t)(d.rows * d.cols);
       Writer C{out + d.dst, d.rows, d.cols, (uint32_t)(d.cols / 16), unit_aligned(0, n, d.rows, d.cols)};
-      err = run_stream(S, lane, arc + d.src, arc + d.src + d.size, n, 0, P, C, has_next ? arc + dn.src : nullptr,
-                       arc + dn.src + dn.size, (uint32_t)(dn.rows * dn.cols), PN);
+      err = run_stream(S, lane, arc + d.src, arc + d.src + d.size, n, 0, C,
+                       NextStream{has_next ? arc + dn.src : nullptr, arc + dn.src + dn.size,
+                                  (uint32_t)(dn.rows * dn.cols)},
+                       PN);
     } else if (has_next) {
       issue_stream(PN, arc + dn.src, arc + dn.src + dn.size, (uint32_t)(dn.rows * dn.cols), lane);
+      drain_loads();
+      stage_inputs(S, lane, PN);
     }
-    P = PN;
     set_status(status, d.status_slot, err, lane);
   }
 }
@@ -1201,9 +1292,13 @@ __global__ void __launch_bounds__(64 * W) k_gemm(const DevBlock* __restrict__ bl
         for (uint32_t q = 0; q < k && q < chunks; ++q) off += rdlane64(hv, 4 + q);
         len = k < chunks ? rdlane64(hv, 4 + k) : 0;
       }
-      StreamIn P, PN;
-      if (k < chunks)
-        issue_stream(P, blk + off, blk + off + len, (uint32_t)(total * (k + 1) / chunks - total * k / chunks), lane);
+      StreamIn PN;
+      if (k < chunks) {
+        issue_stream(PN, blk + off, blk + off + len, (uint32_t)(total * (k + 1) / chunks - total * k / chunks),
+                     lane);
+        drain_loads();
+        stage_inputs(S, lane, PN);
+      }
       for (; k < chunks && !err; k += W) {
         const uint32_t s0 = (uint32_t)(total * k / chunks), s1 = (uint32_t)(total * (k + 1) / chunks);
         // next substream of this wave
@@ -1220,10 +1315,9 @@ __global__ void __launch_bounds__(64 * W) k_gemm(const DevBlock* __restrict__ bl
         }
         Acc C(ga);
         C.init();
-        err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, P, C, kn < chunks ? blk + noff : nullptr,
-                         blk + noff + nlen, ncount, PN);
+        err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, C,
+                         NextStream{kn < chunks ? blk + noff : nullptr, blk + noff + nlen, ncount}, PN);
         C.deposit(red[w], lane, s0);
-        P = PN;
         off = noff;
         len = nlen;
       }
