@@ -56,8 +56,9 @@ constexpr uint64_t kMagicXKSP2 = 0x0000003250534B58ull;  // "XKSP2\0\0\0" little
 // limits) or the bit-serial tables; rank/compaction scratch lives in `syms`
 // before decoding starts.
 // Two-symbol lookup entry for a 10-bit window (0 = first code longer than 10
-// bits, or invalid):  bits 0-7 first symbol, 8-15 second symbol, 16-22 bits
-// consumed, 23 second symbol present, 24-27 length of the first code.
+// bits, or invalid):  bits 0-7 first symbol, 8-14 bits consumed, 15 second
+// symbol present, 16-23 second symbol, 24-27 length of the first code.  The
+// two symbols sit in the bytes a byte store and a high-half byte store write.
 struct FastTables {
   uint32_t lut2[1u << kLutBits];
   uint64_t lim[40];              // lim[l] = left-aligned 32-bit end of the length-l codes, C(l+1)
@@ -368,7 +369,7 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
       const uint32_t l2 = b >> 8;
       const bool two = v != 0 && b != 0 && l1 + l2 <= kLutBits;
       o[i] = v == 0 ? 0u
-                    : (v & 255u) | (two ? (b & 255u) << 8 : 0u) | ((two ? l1 + l2 : l1) << 16) | (two ? 1u << 23 : 0u) |
+                    : (v & 255u) | ((two ? l1 + l2 : l1) << 8) | (two ? 1u << 15 : 0u) | (two ? (b & 255u) << 16 : 0u) |
                           (l1 << 24);
     }
     *reinterpret_cast<uint4*>(&F.lut2[16 * lane + 4 * g]) = make_uint4(o[0], o[1], o[2], o[3]);
@@ -449,45 +450,55 @@ struct Path {
 };
 constexpr uint32_t kNoStart = 0xffffffffu;
 
-// Slide the register window (w0, w1, w2 = segment dwords (p+31)/32 - 1 ..
-// +1) after p advanced from `from` by at most 32 bits; the third dword is
+// Slide the register window (w0, w1, w2 = segment dwords wi - 1 .. wi + 1,
+// wi = (p + 31) / 32) after p advanced by at most 32 bits; the third dword is
 // re-read from LDS off the dependency chain.
-__device__ __forceinline__ void slide(const Smem& S, uint32_t from, uint32_t p, uint32_t& w0, uint32_t& w1,
+__device__ __forceinline__ void slide(const Smem& S, uint32_t p, uint32_t& wi, uint32_t& w0, uint32_t& w1,
                                       uint32_t& w2) {
   const uint32_t i1 = (p + 31) >> 5;
-  const bool adv = i1 != ((from + 31) >> 5);
+  const bool adv = i1 != wi;
+  wi = i1;
   w0 = adv ? w1 : w0;
   w1 = adv ? w2 : w1;
   w2 = S.stream[i1 + 2];
 }
 
-// Up to two codewords at bit p (lut2 entry layout); a second codeword that
-// would start at or past `end` is left for the caller.  A window that matches
-// no code sets `dead` and moves p to `end`, which ends the caller's loop.
-__device__ __forceinline__ uint32_t step2(const Smem& S, uint32_t& p, uint32_t end, uint32_t& w0, uint32_t& w1,
-                                          uint32_t& w2, uint32_t maxlen, uint32_t& dead) {
+// Up to two codewords at bit p (lut2 entry layout).  A window that matches no
+// code sets `dead` and moves p to `end`, which ends the caller's loop.  The
+// second codeword may start at or past `end`; the caller's loop undoes that
+// after its last step (end_pair).
+__device__ __forceinline__ uint32_t step2(const Smem& S, uint32_t& p, uint32_t end, uint32_t& wi, uint32_t& w0,
+                                          uint32_t& w1, uint32_t& w2, uint32_t maxlen, uint32_t& dead) {
   const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
   uint32_t e = S.t.f.lut2[win >> (32 - kLutBits)];
   if (e == 0) {
     const uint32_t lc = long_code(S, win, maxlen);
     const uint32_t len = lc ? lc >> 8 : end - p;
     dead |= lc == 0;
-    e = (lc & 255u) | (len << 16) | (len << 24);
+    e = (lc & 255u) | (len << 8);
   }
-  const uint32_t l1 = (e >> 24) & 15u;
-  const bool cut = ((e >> 23) & 1u) && p + l1 >= end;
-  e = cut ? (e & 0x0f0000ffu) | (l1 << 16) : e;
-  const uint32_t from = p;
-  p += (e >> 16) & 127u;
-  slide(S, from, p, w0, w1, w2);
+  p += (e >> 8) & 127u;
+  slide(S, p, wi, w0, w1, w2);
   return e;
 }
 
-__device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
-  const uint32_t i = (p + 31) >> 5;
-  w0 = S.stream[i];
-  w1 = S.stream[i + 1];
-  w2 = S.stream[i + 2];
+// After a loop of step2 calls that stopped at the first p >= end: when its
+// last step (at bit lp, entry le) was a pair whose second codeword starts at
+// or past `end`, that codeword belongs to the next range: step back to it.
+// Returns 1 when a symbol was taken back.
+__device__ __forceinline__ uint32_t end_pair(uint32_t lp, uint32_t le, uint32_t end, uint32_t& p) {
+  const uint32_t s2 = lp + ((le >> 24) & 15u);
+  const bool back = ((le >> 15) & 1u) && s2 >= end;
+  p = back ? s2 : p;
+  return back;
+}
+
+__device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t& wi, uint32_t& w0, uint32_t& w1,
+                                            uint32_t& w2) {
+  wi = (p + 31) >> 5;
+  w0 = S.stream[wi];
+  w1 = S.stream[wi + 1];
+  w2 = S.stream[wi + 2];
 }
 
 // Decode the codewords that start in [cs, ce) into region[0 ...], two per
@@ -498,18 +509,28 @@ __device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t&
 // lane's exit).  Symbols are stored a byte at a time (aligned LDS stores).
 __device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint32_t cs, uint32_t ce, uint8_t* region,
                                              uint32_t maxlen, Path& P) {
-  uint32_t p = from, c = 0, d = 0, w0, w1, w2;
-  load_window(S, p, w0, w1, w2);
-  while (p < cs) step2(S, p, cs, w0, w1, w2, maxlen, d);
+  uint32_t p = from, c = 0, d = 0, wi, w0, w1, w2, lp = p, le = 0;
+  load_window(S, p, wi, w0, w1, w2);
+  if (p < cs) {
+    while (p < cs) {
+      lp = p;
+      le = step2(S, p, cs, wi, w0, w1, w2, maxlen, d);
+    }
+    end_pair(lp, le, cs, p);
+    load_window(S, p, wi, w0, w1, w2);
+  }
   P.f = d ? kNoStart : p;
   if (d) p = ce;
   lds_bytes out = as_lds(region);
+  le = 0;
   while (p < ce) {
-    const uint32_t e = step2(S, p, ce, w0, w1, w2, maxlen, d);
-    out[c] = (uint8_t)e;
-    out[c + 1] = (uint8_t)(e >> 8);
-    c += 1 + ((e >> 23) & 1u);
+    lp = p;
+    le = step2(S, p, ce, wi, w0, w1, w2, maxlen, d);
+    out[c] = (uint8_t)le;
+    out[c + 1] = (uint8_t)(le >> 16);
+    c += 1 + ((le >> 15) & 1u);
   }
+  c -= end_pair(lp, le, ce, p);
   P.cnt = c;
   P.ex = p;
   P.dead = d;
