@@ -355,24 +355,28 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
   }
   wave_sync();
   // Two-symbol table: entry e holds its first code and, when the code after
-  // it also ends within the 10-bit window, that one too.
+  // it also ends within the 10-bit window, that one too.  Lane l takes
+  // entries l + 64 i, so both the entry reads and the second-code reads
+  // (index (e << l1) mod 1024, consecutive lanes 2^l1 entries apart) spread
+  // over the LDS banks.
+  const uint16_t* lut1r = lut1;
 #pragma unroll
-  for (uint32_t g = 0; g < 4; ++g) {  // four entries at a time keeps register use low
-    const uint2 a = *reinterpret_cast<const uint2*>(&lut1[16 * lane + 4 * g]);
-    uint32_t o[4];
+  for (uint32_t g = 0; g < 2; ++g) {  // eight entries at a time: two LDS round trips per group
+    uint32_t v[8], b[8];
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-      const uint32_t e = 16 * lane + 4 * g + i;
-      const uint32_t v = ((i < 2 ? a.x : a.y) >> (16 * (i & 1))) & 0xffffu;
-      const uint32_t l1 = v >> 8;
-      const uint32_t b = lut1[(e << l1) & ((1u << kLutBits) - 1)];
-      const uint32_t l2 = b >> 8;
-      const bool two = v != 0 && b != 0 && l1 + l2 <= kLutBits;
-      o[i] = v == 0 ? 0u
-                    : (v & 255u) | ((two ? l1 + l2 : l1) << 8) | (two ? 1u << 15 : 0u) | (two ? (b & 255u) << 16 : 0u) |
-                          (l1 << 24);
+    for (uint32_t i = 0; i < 8; ++i) v[i] = lut1r[lane + kWave * (8 * g + i)];
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i)
+      b[i] = lut1r[((lane + kWave * (8 * g + i)) << (v[i] >> 8)) & ((1u << kLutBits) - 1)];
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      const uint32_t l1 = v[i] >> 8, l2 = b[i] >> 8;
+      const bool two = v[i] != 0 && b[i] != 0 && l1 + l2 <= kLutBits;
+      F.lut2[lane + kWave * (8 * g + i)] =
+          v[i] == 0 ? 0u
+                    : (v[i] & 255u) | ((two ? l1 + l2 : l1) << 8) | (two ? 1u << 15 : 0u) |
+                          (two ? (b[i] & 255u) << 16 : 0u) | (l1 << 24);
     }
-    *reinterpret_cast<uint4*>(&F.lut2[16 * lane + 4 * g]) = make_uint4(o[0], o[1], o[2], o[3]);
   }
   wave_sync();
   return Book{0, maxlen, true};
@@ -683,26 +687,39 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
       const uint32_t dst = carry + tinc - t;
       const uint32_t dh = dst & 3u, nq = (t + 3) >> 2, nqmax = wave_max(nq);
       const uint32_t* src = reinterpret_cast<const uint32_t*>(region);
-      uint32_t R[kChunk / 4];
+      // Four dwords per step under a wave-uniform bound (no register
+      // indexing); bytes past a lane's run are read but never stored.
+      constexpr uint32_t kQ = kChunk / 4;
+      uint32_t R[kQ + 4];
 #pragma unroll
-      for (uint32_t q = 0; q < kChunk / 4; ++q) {
-        if (q >= nqmax) break;
-        R[q] = q < nq ? src[q] : 0u;
+      for (uint32_t q0 = 0; q0 < kQ; q0 += 4) {
+        if (q0 < nqmax) {
+#pragma unroll
+          for (uint32_t q = q0; q < q0 + 4; ++q) R[q] = src[q];
+        } else {
+#pragma unroll
+          for (uint32_t q = q0; q < q0 + 4; ++q) R[q] = 0u;
+        }
       }
+#pragma unroll
+      for (uint32_t q = kQ; q < kQ + 4; ++q) R[q] = 0u;
       wave_sync();
       uint32_t* d32 = reinterpret_cast<uint32_t*>(S.syms + (dst & ~3u));
       const uint32_t sh = (4u - dh) & 3u;  // destination dword k = run bytes [4k - dh, 4k - dh + 4)
       const uint32_t nw = (dh + t) >> 2;   // destination dwords that end inside the run
-      uint32_t head = 0, tail = 0, prev = 0;
+      uint32_t head = 0, tail = 0;
 #pragma unroll
-      for (uint32_t k = 0; k <= kChunk / 4; ++k) {
-        if (k > nqmax) break;
-        const uint32_t cur = k < nq ? R[k < kChunk / 4 ? k : 0] : 0u;
-        const uint32_t w = dh ? __builtin_amdgcn_alignbyte(cur, prev, sh) : cur;
-        if (k == 0) head = w;
-        if (k == nw) tail = w;
-        if (k < nw && (k > 0 || dh == 0)) d32[k] = w;
-        prev = cur;
+      for (uint32_t k0 = 0; k0 <= kQ; k0 += 4) {
+        if (k0 <= nqmax) {
+#pragma unroll
+          for (uint32_t k = k0; k < k0 + 4; ++k) {
+            const uint32_t cur = R[k], prev = k ? R[k - 1] : 0u;
+            const uint32_t w = dh ? __builtin_amdgcn_alignbyte(cur, prev, sh) : cur;
+            if (k == 0) head = w;
+            tail = k == nw ? w : tail;
+            if (k < nw && (k > 0 || dh == 0)) d32[k] = w;
+          }
+        }
       }
       lds_bytes d8 = as_lds(S.syms + (dst & ~3u));
       // Head: bytes dh..3 of dword 0 (when the run does not start aligned).
