@@ -157,27 +157,42 @@ __device__ __forceinline__ uint32_t ldg32(const uint8_t* p) {
   __builtin_memcpy(&v, p, 4);
   return v;
 }
-// 16 bytes at p; bytes at or past `end` read as zero.  One 16-byte load that
-// never crosses `end`: near the end it reads the 16 bytes before `end` and
-// shifts.  Callers guarantee [end - 16, end) is inside the same buffer (every
-// segment holds at least 272 header bytes before its code bytes).
-__device__ __forceinline__ uint4 ldg16_bounded(const uint8_t* p, const uint8_t* end) {
-  if (p >= end) return make_uint4(0u, 0u, 0u, 0u);
-  const uint8_t* q = p + 16 <= end ? p : end - 16;
+// 16 bytes at p with the bytes at or past `end` reading as zero, in two
+// halves so that issuing the load does not wait for it: fetch16() issues one
+// 16-byte load that never crosses `end` (near the end it reads the 16 bytes
+// before `end`) and records how many leading bytes to drop; value() shifts
+// them out once the data is needed.  Callers guarantee [end - 16, end) is
+// inside the same buffer (every segment holds 272 header bytes before its
+// code bytes).
+struct Fetch16 {
   uint4 v;
-  __builtin_memcpy(&v, q, 16);
-  const uint32_t sh = (uint32_t)(p - q), d = sh >> 2, r = sh & 3u;  // drop the first sh bytes
-  const uint32_t w[5] = {v.x, v.y, v.z, v.w, 0u};
-  uint32_t o[4];
+  uint32_t drop;  // leading bytes to drop; 16 = none of the bytes are wanted
+  __device__ __forceinline__ uint4 value() const {
+    const uint32_t d = drop >> 2, r = drop & 3u;
+    const uint32_t w[5] = {v.x, v.y, v.z, v.w, 0u};
+    uint32_t o[4];
 #pragma unroll
-  for (uint32_t k = 0; k < 4; ++k) {
-    const uint32_t lo = d == 0 ? w[k] : d == 1 ? w[k + 1 < 5 ? k + 1 : 4] : d == 2 ? w[k + 2 < 5 ? k + 2 : 4]
-                                                                                    : w[k + 3 < 5 ? k + 3 : 4];
-    const uint32_t hi = d == 0 ? w[k + 1 < 5 ? k + 1 : 4] : d == 1 ? w[k + 2 < 5 ? k + 2 : 4]
-                                                                    : d == 2 ? w[k + 3 < 5 ? k + 3 : 4] : 0u;
-    o[k] = r ? __builtin_amdgcn_alignbyte(hi, lo, r) : lo;
+    for (uint32_t k = 0; k < 4; ++k) {
+      const uint32_t lo = d == 0 ? w[k] : d == 1 ? w[k + 1 < 5 ? k + 1 : 4] : d == 2 ? w[k + 2 < 5 ? k + 2 : 4]
+                                                  : d == 3 ? w[k + 3 < 5 ? k + 3 : 4] : 0u;
+      const uint32_t hi = d == 0 ? w[k + 1 < 5 ? k + 1 : 4] : d == 1 ? w[k + 2 < 5 ? k + 2 : 4]
+                                                            : d == 2 ? w[k + 3 < 5 ? k + 3 : 4] : 0u;
+      o[k] = r ? __builtin_amdgcn_alignbyte(hi, lo, r) : lo;
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
   }
-  return make_uint4(o[0], o[1], o[2], o[3]);
+};
+__device__ __forceinline__ Fetch16 fetch16(const uint8_t* p, const uint8_t* end) {
+  Fetch16 f;
+  if (p >= end) {
+    f.v = make_uint4(0u, 0u, 0u, 0u);
+    f.drop = 16;
+    return f;
+  }
+  const uint8_t* q = p + 16 <= end ? p : end - 16;
+  __builtin_memcpy(&f.v, q, 16);
+  f.drop = (uint32_t)(p - q);
+  return f;
 }
 __device__ __forceinline__ uint32_t lds32(const uint8_t* p) {
   uint32_t v;
@@ -546,7 +561,7 @@ __device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint3
 struct StreamIn {
   uint64_t hdr;
   uint32_t lens;
-  uint4 bits;
+  Fetch16 bits;
 };
 // Sign/mantissa bytes of the first 256 units (2048 positions) a consume call
 // will see: unit lane_unit(lane) + 64 i in v[i] (the consumer's own mapping).
@@ -561,8 +576,12 @@ __device__ __forceinline__ void issue_stream(StreamIn& P, const uint8_t* seg, co
                                              uint32_t lane) {
   P.hdr = lane < 2 ? ldg64(seg + 8 * lane) : 0ull;
   P.lens = ldg32(seg + 16 + 4 * lane);
-  P.bits = lane < kStreamLanes ? ldg16_bounded(seg + 272 + (uint64_t)count + 16 * lane, seg_end)
-                               : make_uint4(0u, 0u, 0u, 0u);
+  if (lane < kStreamLanes) {
+    P.bits = fetch16(seg + 272 + (uint64_t)count + 16 * lane, seg_end);
+  } else {
+    P.bits.v = make_uint4(0u, 0u, 0u, 0u);
+    P.bits.drop = 16;
+  }
 }
 __device__ __forceinline__ void issue_sm(SmWin& W, const uint8_t* sm, uint32_t pos0, uint32_t count, uint32_t lu) {
 #pragma unroll
@@ -606,7 +625,7 @@ __device__ __forceinline__ void stage_bits(Smem& S, uint32_t lane, uint4 v) {
 // drain_loads() -- so the next stream starts without waiting on the memory
 // counter, which by then also counts this stream's output stores.
 __device__ __forceinline__ void stage_inputs(Smem& S, uint32_t lane, const StreamIn& P) {
-  stage_bits(S, lane, P.bits);
+  stage_bits(S, lane, P.bits.value());
   if (lane == 0) S.stream[0] = 0;
   reinterpret_cast<uint32_t*>(S.sorted)[lane] = P.lens;
   if (lane < 2) reinterpret_cast<uint64_t*>(S.bcast)[lane] = P.hdr;
@@ -625,17 +644,19 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
   uint8_t* const region = S.syms + kCarry + lane * kRegion;
   uint32_t carry = 0, pos0 = 0, entry = 0, err = 0;
   uint64_t S0 = 0, true_pos = 0;
-  uint4 cur = make_uint4(0u, 0u, 0u, 0u);
+  Fetch16 cur;
+  cur.v = make_uint4(0u, 0u, 0u, 0u);
+  cur.drop = 16;
   bool staged = false;
   while (true_pos < nbits) {
     if (S0) {  // the first segment's bytes were staged with the stream's inputs
-      stage_bits(S, lane, cur);
+      stage_bits(S, lane, cur.value());
       wave_sync();
     }
     // Next segment's code bytes and this segment's sign/mantissa window go
     // out now and land while the segment decodes.
     if (S0 + kSegBits < nbits && lane < kStreamLanes)
-      cur = ldg16_bounded(st.bits + ((S0 + kSegBits) >> 3) + 16 * lane, bend);
+      cur = fetch16(st.bits + ((S0 + kSegBits) >> 3) + 16 * lane, bend);
     SmWin W;
     issue_sm(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
     const uint64_t left = nbits - S0;
