@@ -43,6 +43,8 @@ constexpr uint32_t kSymsBytes = kCarry + kWave * kRegion;
 constexpr uint32_t kStreamDw = kSegBits / 32 + 2;   // segment dwords plus lookahead
 constexpr uint32_t kStreamLanes = (kStreamDw + 3) / 4;
 constexpr uint32_t kLutBits = 10;
+constexpr uint32_t kLongLen = 127;
+constexpr uint32_t kLongMark = kLongLen << 8;
 constexpr uint32_t kMaxLenFast = 32;
 constexpr uint32_t kSlowSeg = 4096;                 // symbols per bit-serial segment (multiple of 256)
 constexpr uint64_t kMagicXKSP2 = 0x0000003250534B58ull;  // "XKSP2\0\0\0" little-endian
@@ -55,10 +57,13 @@ constexpr uint64_t kMagicXKSP2 = 0x0000003250534B58ull;  // "XKSP2\0\0\0" little
 // Per-wave LDS.  The table area is either the fast tables (LUT + per-length
 // limits) or the bit-serial tables; rank/compaction scratch lives in `syms`
 // before decoding starts.
-// Two-symbol lookup entry for a 10-bit window (0 = first code longer than 10
-// bits, or invalid):  bits 0-7 first symbol, 8-14 bits consumed, 15 second
-// symbol present, 16-23 second symbol, 24-27 length of the first code.  The
-// two symbols sit in the bytes a byte store and a high-half byte store write.
+// Two-symbol lookup entry for a 10-bit window: bits 0-7 first symbol, 8-14
+// bits consumed, 15 second symbol present, 16-23 second symbol, 24-27 length
+// of the first code.  The two symbols sit in the bytes a byte store and a
+// high-half byte store write.  A window whose first code is longer than 10
+// bits (or matches no code) holds kLongMark: "consumed" 127 moves the bit
+// position past the end of any chunk, which ends the decode loop for that
+// lane without a branch in the loop; the code is resolved after the loop.
 struct FastTables {
   uint32_t lut2[1u << kLutBits];
   uint64_t lim[40];              // lim[l] = left-aligned 32-bit end of the length-l codes, C(l+1)
@@ -388,7 +393,7 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
       const uint32_t l1 = v[i] >> 8, l2 = b[i] >> 8;
       const bool two = v[i] != 0 && b[i] != 0 && l1 + l2 <= kLutBits;
       F.lut2[lane + kWave * (8 * g + i)] =
-          v[i] == 0 ? 0u
+          v[i] == 0 ? kLongMark
                     : (v[i] & 255u) | ((two ? l1 + l2 : l1) << 8) | (two ? 1u << 15 : 0u) |
                           (two ? (b[i] & 255u) << 16 : 0u) | (l1 << 24);
     }
@@ -482,30 +487,27 @@ __device__ __forceinline__ void slide(const Smem& S, uint32_t p, uint32_t& wi, u
   w2 = S.stream[i1 + 2];
 }
 
-// Up to two codewords at bit p (lut2 entry layout).  A window that matches no
-// code sets `dead` and moves p to `end`, which ends the caller's loop.  The
-// second codeword may start at or past `end`; the caller's loop undoes that
-// after its last step (end_pair).
-__device__ __forceinline__ uint32_t step2(const Smem& S, uint32_t& p, uint32_t end, uint32_t& wi, uint32_t& w0,
-                                          uint32_t& w1, uint32_t& w2, uint32_t maxlen, uint32_t& dead) {
+// Up to two codewords at bit p (lut2 entry layout).  A window without a code
+// of at most 10 bits moves p by kLongLen (past the caller's end); the caller
+// resolves it (resolve_long).  The second codeword may start at or past the
+// caller's end; the caller undoes that after its last step (end_pair).
+// Bit positions stay below kSegBits + kLongLen + 32, inside the staged
+// segment buffer.
+__device__ __forceinline__ uint32_t step2(const Smem& S, uint32_t& p, uint32_t& wi, uint32_t& w0, uint32_t& w1,
+                                          uint32_t& w2) {
   const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
-  uint32_t e = S.t.f.lut2[win >> (32 - kLutBits)];
-  if (e == 0) {
-    const uint32_t lc = long_code(S, win, maxlen);
-    const uint32_t len = lc ? lc >> 8 : end - p;
-    dead |= lc == 0;
-    e = (lc & 255u) | (len << 8);
-  }
+  const uint32_t e = S.t.f.lut2[win >> (32 - kLutBits)];
   p += (e >> 8) & 127u;
   slide(S, p, wi, w0, w1, w2);
   return e;
 }
 
-// After a loop of step2 calls that stopped at the first p >= end: when its
-// last step (at bit lp, entry le) was a pair whose second codeword starts at
-// or past `end`, that codeword belongs to the next range: step back to it.
-// Returns 1 when a symbol was taken back.
-__device__ __forceinline__ uint32_t end_pair(uint32_t lp, uint32_t le, uint32_t end, uint32_t& p) {
+// After a loop of step2 calls that stopped at the first p >= end, with `le`
+// the last step's entry: when that step was a pair whose second codeword
+// starts at or past `end`, that codeword belongs to the next range: step
+// back to it.  Returns 1 when a symbol was taken back.
+__device__ __forceinline__ uint32_t end_pair(uint32_t le, uint32_t end, uint32_t& p) {
+  const uint32_t lp = p - ((le >> 8) & 127u);
   const uint32_t s2 = lp + ((le >> 24) & 15u);
   const bool back = ((le >> 15) & 1u) && s2 >= end;
   p = back ? s2 : p;
@@ -520,37 +522,70 @@ __device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t&
   w2 = S.stream[wi + 2];
 }
 
+// The last step's entry `le` was kLongMark: move p back to that step's start
+// and decode the code there with the per-length limits.  A window that
+// matches no code sets `dead` and moves p to `end`.  Returns the code as
+// (len << 8) | symbol, or 0 when dead; `le` becomes a one-symbol entry.
+__device__ __forceinline__ uint32_t resolve_long(const Smem& S, uint32_t& p, uint32_t end, uint32_t& le,
+                                                 uint32_t maxlen, uint32_t& dead, uint32_t& wi, uint32_t& w0,
+                                                 uint32_t& w1, uint32_t& w2) {
+  p -= kLongLen;
+  load_window(S, p, wi, w0, w1, w2);
+  const uint32_t lc = long_code(S, __builtin_amdgcn_alignbit(w0, w1, 0u - p), maxlen);
+  if (lc) {
+    p += lc >> 8;
+    le = lc;  // bits 8-14 = length, no second symbol
+  } else {
+    dead = 1;
+    p = end;
+    le = 0;
+  }
+  load_window(S, p, wi, w0, w1, w2);
+  return lc;
+}
+
 // Decode the codewords that start in [cs, ce) into region[0 ...], two per
 // lookup where the table allows.  When `from` < cs the codewords before cs
 // are decoded and dropped: Huffman codes resynchronise within a few
 // codewords, so a path started kSync bits early almost always meets the true
 // codeword boundaries before cs (the caller verifies it against the previous
 // lane's exit).  Symbols are stored a byte at a time (aligned LDS stores).
+// Codes longer than the table end a lane's inner loop (kLongMark); they are
+// decoded between rounds of it, which every lane takes part in.
 __device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint32_t cs, uint32_t ce, uint8_t* region,
                                              uint32_t maxlen, Path& P) {
-  uint32_t p = from, c = 0, d = 0, wi, w0, w1, w2, lp = p, le = 0;
+  uint32_t p = from, d = 0, wi, w0, w1, w2, le = 0;
   load_window(S, p, wi, w0, w1, w2);
   if (p < cs) {
-    while (p < cs) {
-      lp = p;
-      le = step2(S, p, cs, wi, w0, w1, w2, maxlen, d);
+    for (;;) {
+      while (p < cs) le = step2(S, p, wi, w0, w1, w2);
+      const bool lng = le == kLongMark;
+      if (!__ballot(lng)) break;
+      if (lng) resolve_long(S, p, cs, le, maxlen, d, wi, w0, w1, w2);
     }
-    end_pair(lp, le, cs, p);
+    end_pair(le, cs, p);
     load_window(S, p, wi, w0, w1, w2);
   }
   P.f = d ? kNoStart : p;
   if (d) p = ce;
-  lds_bytes out = as_lds(region);
+  lds_bytes const out = as_lds(region);
+  lds_bytes o = out;  // next symbol slot
   le = 0;
-  while (p < ce) {
-    lp = p;
-    le = step2(S, p, ce, wi, w0, w1, w2, maxlen, d);
-    out[c] = (uint8_t)le;
-    out[c + 1] = (uint8_t)(le >> 16);
-    c += 1 + ((le >> 15) & 1u);
+  for (;;) {
+    while (p < ce) {
+      le = step2(S, p, wi, w0, w1, w2);
+      o[0] = (uint8_t)le;
+      o[1] = (uint8_t)(le >> 16);
+      o += 1 + ((le >> 15) & 1u);
+    }
+    const bool lng = le == kLongMark;
+    if (!__ballot(lng)) break;
+    if (lng) {  // the marker step stored one junk symbol at o[-1]
+      const uint32_t lc = resolve_long(S, p, ce, le, maxlen, d, wi, w0, w1, w2);
+      o[-1] = (uint8_t)lc;
+    }
   }
-  c -= end_pair(lp, le, ce, p);
-  P.cnt = c;
+  P.cnt = (uint32_t)(o - out) - end_pair(le, ce, p);
   P.ex = p;
   P.dead = d;
 }
