@@ -598,10 +598,14 @@ struct StreamIn {
   uint32_t lens;
   Fetch16 bits;
 };
-// Sign/mantissa bytes of the first 256 units (2048 positions) a consume call
-// will see: unit lane_unit(lane) + 64 i in v[i] (the consumer's own mapping).
+// Sign/mantissa bytes of the first kSmWin * 64 units (3,072 positions) a
+// consume call will see: unit lane_unit(lane) + 64 i in v[i] (the consumer's
+// own mapping).  A full 6,144-bit segment of codes averaging 2-2.6 bits holds
+// 2,400-3,100 symbols; units past the window are loaded inside the call,
+// which then waits for the loads (and for any stores issued before them).
+constexpr uint32_t kSmWin = 6;
 struct SmWin {
-  uint64_t v[4];
+  uint64_t v[kSmWin];
 };
 
 // `seg` .. `seg_end` is one serial block or XKSP2 segment; `count` is the
@@ -620,7 +624,7 @@ __device__ __forceinline__ void issue_stream(StreamIn& P, const uint8_t* seg, co
 }
 __device__ __forceinline__ void issue_sm(SmWin& W, const uint8_t* sm, uint32_t pos0, uint32_t count, uint32_t lu) {
 #pragma unroll
-  for (uint32_t i = 0; i < 4; ++i) {
+  for (uint32_t i = 0; i < kSmWin; ++i) {
     const uint32_t p = pos0 + 8 * (lu + kWave * i);
     W.v[i] = p + 8 <= count ? ldg64(sm + p) : 0ull;
   }
@@ -969,11 +973,12 @@ struct Writer {
     const uint32_t take = final ? avail : (avail & ~255u);
     const uint32_t units = take >> 3;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
+    for (uint32_t i = 0; i < kSmWin; ++i) {
       const uint32_t u = lane + kWave * i;
       if (u < units) unit(S, st, pos0, u, W.v[i]);
     }
-    for (uint32_t u = lane + 4 * kWave; u < units; u += kWave) unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
+    for (uint32_t u = lane + kSmWin * kWave; u < units; u += kWave)
+      unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
     return take;
   }
 };
@@ -1050,11 +1055,12 @@ struct GemmF32 {
     const uint32_t take = final ? avail : (avail & ~255u);
     const uint32_t units = take >> 3;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
+    for (uint32_t i = 0; i < kSmWin; ++i) {
       const uint32_t u = lane + kWave * i;
       if (u < units) unit(S, st, pos0, u, W.v[i]);
     }
-    for (uint32_t u = lane + 4 * kWave; u < units; u += kWave) unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
+    for (uint32_t u = lane + kSmWin * kWave; u < units; u += kWave)
+      unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
     return take;
   }
   // Four lanes share each row: with s = (stream start / 8) % 2, lane l and
@@ -1130,11 +1136,12 @@ struct GemmBf16 {
     const uint32_t take = final ? avail : (avail & ~255u);
     const uint32_t units = take >> 3;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
+    for (uint32_t i = 0; i < kSmWin; ++i) {
       const uint32_t u = lane + kWave * i;
       if (u < units) unit(S, st, pos0, u, W.v[i]);
     }
-    for (uint32_t u = lane + 4 * kWave; u < units; u += kWave) unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
+    for (uint32_t u = lane + kSmWin * kWave; u < units; u += kWave)
+      unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
     return take;
   }
   __device__ __forceinline__ void deposit(float* slots, uint32_t lane, uint32_t s0) {
@@ -1193,7 +1200,7 @@ struct GemmMfma {
       uint64_t E = 0, M = 0;
       if (valid) {
         __builtin_memcpy(&E, S.syms + 8 * u, 8);
-        M = b < 4 ? W.v[b] : ldg64(st.sm + pos0 + 8 * u);
+        M = b < kSmWin ? W.v[b] : ldg64(st.sm + pos0 + 8 * u);
       }
       const uint4 w = combine8(E, M);
       uint4 xv = make_uint4(0u, 0u, 0u, 0u);
