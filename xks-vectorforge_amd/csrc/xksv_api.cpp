@@ -23,6 +23,9 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 constexpr uint64_t kAlign = 256;
+// Largest substream partial-sum scratch a plan allocates (32 KiB per fused
+// XKSP2 block: 32,768 blocks, a 4 GiB BF16 weight set).
+constexpr uint64_t kMaxItemMem = 1ull << 30;
 constexpr uint64_t kQueues = 4;  // block-queue counters per plan (one per decode launch of a step)
 
 uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
@@ -122,7 +125,9 @@ int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows
   if (!di) return 1;
   const uint64_t n = rows * cols;
   const bool generic_gemm = mode != kDecode && !fused.unit;
-  Layout L(size, generic_gemm ? n * 2 : 0);
+  // Fused GEMM over an XKSP2 block runs by substream (item scratch).
+  const bool items = mode != kDecode && !generic_gemm && codec == kCodecParallel;
+  Layout L(size, generic_gemm ? n * 2 : items ? kItemScratchPerBlock : 0);
   Buf b;
   if (!acquire(dev, L.total, b)) return 1;
   int rc = 1;
@@ -136,6 +141,8 @@ int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows
     if (launch_fill_u32(status, kAlign / 4, 0, nullptr) != hipSuccess) break;
     const DevBlock* dd = reinterpret_cast<const DevBlock*>(b.p + L.desc);
     const unsigned cus = (unsigned)di->cus;
+    const ItemScratch is{reinterpret_cast<float*>(b.p + L.scratch),
+                         reinterpret_cast<uint32_t*>(b.p + L.scratch + kItemScratchPerBlock - 4)};
     float* y = static_cast<float*>(out);
     if (mode == kDecode) {
       if (launch_decode(dd, 1, codec, b.p, static_cast<uint8_t*>(out), status, nullptr, cus, nullptr) != hipSuccess)
@@ -146,10 +153,11 @@ int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows
         const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
         if (mode == kGemmF32)
           ok = launch_gemm_f32(dd, 1, codec, b.p, static_cast<const float*>(x) + j0, batch, nb, y + j0, batch, status,
-                               cus, nullptr) == hipSuccess;
+                               items ? &is : nullptr, cus, nullptr) == hipSuccess;
         else
           ok = launch_gemm_bf16(dd, 1, codec, b.p, static_cast<const uint16_t*>(x) + j0 * cols, cols, nb,
-                                y + j0 * rows, rows, fused.tile, status, cus, nullptr) == hipSuccess;
+                                y + j0 * rows, rows, fused.tile, status, items ? &is : nullptr, cus,
+                                nullptr) == hipSuccess;
       }
       if (!ok) break;
     } else {
@@ -270,6 +278,8 @@ struct xksv_hip_plan {
   uint32_t n_fserial = 0, n_fparallel = 0, n_gser = 0, n_gpar = 0, n_generic = 0, n_graw = 0;
   bool tile_parallel = false;  // parallel32 slabs split into whole-tile substreams (MFMA consumer)
   uint8_t* scratch = nullptr;
+  uint8_t* item_mem = nullptr;  // ItemScratch of the fused XKSP2 list (none: workgroup-per-block kernels)
+  ItemScratch items{};
   std::vector<uint32_t> h_status;
 };
 
@@ -331,6 +341,14 @@ bool prepare_gemm(xksv_hip_plan* P) {
   // cols / 32 elements: whole tiles when cols is a multiple of 512.
   P->tile_parallel = cols % 512 == 0;
   if (scratch && hipMalloc(reinterpret_cast<void**>(&P->scratch), scratch) != hipSuccess) return false;
+  // Substream partial sums for the fused XKSP2 list: 32 KiB per block, up to
+  // kMaxItemMem; larger lists keep the workgroup-per-block kernels.
+  const uint64_t item_bytes = (uint64_t)P->n_fparallel * kItemScratchPerBlock;
+  if (P->n_fparallel && item_bytes <= kMaxItemMem) {
+    if (hipMalloc(reinterpret_cast<void**>(&P->item_mem), item_bytes) != hipSuccess) return false;
+    P->items.partial = reinterpret_cast<float*>(P->item_mem);
+    P->items.done = reinterpret_cast<uint32_t*>(P->item_mem + (uint64_t)P->n_fparallel * (kItemScratchPerBlock - 4));
+  }
   P->gemm_valid = true;
   return true;
 }
@@ -488,7 +506,7 @@ int xksv_hip_plan_destroy(xksv_hip_plan* P) {
   if (P->device >= 0 && cur != P->device) (void)hipSetDevice(P->device);
   for (void* p : {(void*)P->d_serial, (void*)P->d_parallel, (void*)P->d_raw, (void*)P->status, (void*)P->g_fserial,
                   (void*)P->g_fparallel, (void*)P->g_gser, (void*)P->g_gpar, (void*)P->g_gplain, (void*)P->g_raw,
-                  (void*)P->scratch})
+                  (void*)P->scratch, (void*)P->item_mem})
     if (p) (void)hipFree(p);
   if (cur >= 0 && cur != P->device) (void)hipSetDevice(cur);
   delete P;
@@ -531,19 +549,20 @@ static int plan_gemm(xksv_hip_plan* P, const void* archive, const void* x, size_
   const uint16_t* xb = static_cast<const uint16_t*>(x);
   const uint64_t M = P->rows_extent, K = P->cols;
   if (launch_fill_u32(P->status, P->blocks.size() + kQueues, 0, s) != hipSuccess) return 1;
+  const ItemScratch* items = P->item_mem ? &P->items : nullptr;
   for (uint64_t j0 = 0; j0 < batch; j0 += kMaxFusedBatch) {
     const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
     hipError_t e1, e2;
     if (!bf16) {
       e1 = launch_gemm_f32(P->g_fparallel, P->n_fparallel, kCodecParallel, arc, xf + j0, batch, nb, y + j0, batch,
-                           P->status, cus, s);
+                           P->status, items, cus, s);
       e2 = launch_gemm_f32(P->g_fserial, P->n_fserial, kCodecSerial, arc, xf + j0, batch, nb, y + j0, batch,
-                           P->status, cus, s);
+                           P->status, nullptr, cus, s);
     } else {
       e1 = launch_gemm_bf16(P->g_fparallel, P->n_fparallel, kCodecParallel, arc, xb + j0 * K, K, nb, y + j0 * M, M,
-                            P->tile_parallel, P->status, cus, s);
+                            P->tile_parallel, P->status, items, cus, s);
       e2 = launch_gemm_bf16(P->g_fserial, P->n_fserial, kCodecSerial, arc, xb + j0 * K, K, nb, y + j0 * M, M, true,
-                            P->status, cus, s);
+                            P->status, nullptr, cus, s);
     }
     if (e1 != hipSuccess || e2 != hipSuccess) return 1;
   }

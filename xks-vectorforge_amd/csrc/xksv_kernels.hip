@@ -556,13 +556,14 @@ __device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint3
                                              uint32_t maxlen, Path& P) {
   uint32_t p = from, d = 0, wi, w0, w1, w2, le = 0;
   load_window(S, p, wi, w0, w1, w2);
-  if (p < cs) {
-    for (;;) {
-      while (p < cs) le = step2(S, p, wi, w0, w1, w2);
-      const bool lng = le == kLongMark;
-      if (!__ballot(lng)) break;
-      if (lng) resolve_long(S, p, cs, le, maxlen, d, wi, w0, w1, w2);
-    }
+  const bool sync = p < cs;
+  for (;;) {  // every lane takes part in the votes
+    while (p < cs) le = step2(S, p, wi, w0, w1, w2);
+    const bool lng = le == kLongMark;
+    if (!__ballot(lng)) break;
+    if (lng) resolve_long(S, p, cs, le, maxlen, d, wi, w0, w1, w2);
+  }
+  if (sync) {
     end_pair(le, cs, p);
     load_window(S, p, wi, w0, w1, w2);
   }
@@ -703,9 +704,11 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
     const uint32_t cs = lane * kChunk;
     const bool active = cs < lim_bits;
     const uint32_t ce = active ? min(cs + kChunk, lim_bits) : cs;
-    // Lane 0 starts at the true entry; the others kSync bits before their chunk.
-    Path P{cs, 0, cs, 0};
-    if (active) decode_chunk(S, lane ? cs - kSync : entry, cs, ce, region, maxlen, P);
+    // Lane 0 starts at the true entry; the others kSync bits before their
+    // chunk.  Every lane takes part (decode_chunk has wave-wide votes); an
+    // inactive lane's empty range gives f = ex = cs, cnt = 0.
+    Path P;
+    decode_chunk(S, !active ? cs : lane ? cs - kSync : entry, cs, ce, region, maxlen, P);
     // Resolve: lane i is on the true path when its first start equals its
     // predecessor's exit and the predecessor is.  Lanes that fail re-decode
     // from that exit (rare: a path that did not resynchronise within kSync).
@@ -724,7 +727,10 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
         break;
       }
       if (!bad) break;
-      if (!ok && !pd) decode_chunk(S, pe, cs, ce, region, maxlen, P);
+      const bool redo = !ok && !pd;
+      Path Q;
+      decode_chunk(S, redo ? pe : ce, redo ? cs : ce, ce, region, maxlen, Q);  // empty range unless redo
+      if (redo) P = Q;
     }
     if (err) break;
     const uint32_t t = active ? P.cnt : 0u;
@@ -1441,6 +1447,125 @@ __global__ void __launch_bounds__(64 * W) k_gemm(const DevBlock* __restrict__ bl
   }
 }
 
+// Where work item i (substream i % kMaxChunks of block i / kMaxChunks) lies,
+// from its block's header words (issue_head).  `run` = the item decodes;
+// otherwise err says why not (0: the block has fewer substreams).
+struct ItemLoc {
+  const uint8_t* seg;
+  const uint8_t* end;
+  uint32_t count, s0, chunks, err;
+  bool run;
+};
+template <class Acc>
+__device__ __forceinline__ ItemLoc locate_item(const DevBlock& d, const uint8_t* blk, uint32_t k, uint64_t hv,
+                                               uint32_t lane) {
+  ItemLoc L{nullptr, nullptr, 0u, 0u, 0u, 0u, false};
+  L.err = check_head(hv, d.size, d, lane, L.chunks);
+  if (!L.err && (d.rows != 16 || d.cols % 16)) L.err = kErrShape;
+  if (L.err || k >= L.chunks) return L;
+  const uint64_t len = lane >= 4 && lane < 4 + L.chunks ? hv : 0ull;
+  const uint64_t incl = wave_incl(len, lane);
+  const uint64_t end = 32 + 8ull * L.chunks + rdlane64(incl, 4 + k);
+  const uint64_t total = d.rows * d.cols;
+  L.s0 = (uint32_t)(total * k / L.chunks);
+  L.count = (uint32_t)(total * (k + 1) / L.chunks) - L.s0;
+  L.seg = blk + (end - rdlane64(len, 4 + k));
+  L.end = blk + end;
+  if (!Acc::fits(L.s0, L.count, d.rows, d.cols)) L.err = kErrShape;
+  L.run = !L.err;
+  return L;
+}
+
+// Fused decode-GEMM over XKSP2 blocks of 16-row slabs, one substream per work
+// item: wave w of the grid takes items w, w + gridDim.x, ..., so all
+// resident waves share a layer's blocks x 32 substreams whatever the block
+// count.  Per item a wave decodes the substream into consumer Acc and writes
+// its kOut partial sums to the item's slot; item 0 of each block records the
+// block's substream count.  k_gemm_finish adds the slots.  The next item's
+// inputs and the header of the one after load while an item decodes.
+template <class Acc>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_t* __restrict__ arc, GemmArgs ga,
+             uint32_t* __restrict__ status, ItemScratch is) {
+  __shared__ Smem S;
+  const uint32_t lane = lane_id(), stride = gridDim.x;
+  const uint32_t nitems = nblocks * kMaxChunks;
+  uint32_t i = blockIdx.x;
+  if (i >= nitems) return;
+  uint64_t hv = issue_head(arc + blocks[i / kMaxChunks].src, blocks[i / kMaxChunks].size, lane);
+  uint64_t hvn = i + stride < nitems
+                     ? issue_head(arc + blocks[(i + stride) / kMaxChunks].src, blocks[(i + stride) / kMaxChunks].size, lane)
+                     : 0ull;
+  ItemLoc L = locate_item<Acc>(blocks[i / kMaxChunks], arc + blocks[i / kMaxChunks].src, i % kMaxChunks, hv, lane);
+  StreamIn PN;
+  if (L.run) {
+    issue_stream(PN, L.seg, L.end, L.count, lane);
+    drain_loads();
+    stage_inputs(S, lane, PN);
+  }
+  for (;;) {
+    const uint32_t in = i + stride, inn = in + stride, b = i / kMaxChunks, k = i % kMaxChunks;
+    const DevBlock d = blocks[b];
+    ItemLoc LN{nullptr, nullptr, 0u, 0u, 0u, 0u, false};
+    uint64_t hvnn = 0ull;
+    if (in < nitems) {
+      const DevBlock dn = blocks[in / kMaxChunks];
+      LN = locate_item<Acc>(dn, arc + dn.src, in % kMaxChunks, hvn, lane);
+      if (inn < nitems) hvnn = issue_head(arc + blocks[inn / kMaxChunks].src, blocks[inn / kMaxChunks].size, lane);
+    }
+    if (k == 0 && lane == 0) is.done[b] = L.err ? 0u : L.chunks;
+    if (L.err && (k == 0 || k < L.chunks)) set_status(status, d.status_slot, L.err, lane);
+    if (L.run) {
+      Acc C(ga);
+      C.init();
+      const uint32_t err = run_stream(S, lane, L.seg, L.end, L.count, L.s0, C,
+                                      NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN);
+      float* slots = reinterpret_cast<float*>(S.syms);
+      for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) slots[o] = 0.f;
+      wave_sync();
+      C.deposit(slots, lane, L.s0);
+      wave_sync();
+      float* part = is.partial + (uint64_t)i * kMaxItemOut;
+      for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) part[o] = slots[o];
+      wave_sync();
+      set_status(status, d.status_slot, err, lane);
+    } else if (LN.run) {
+      issue_stream(PN, LN.seg, LN.end, LN.count, lane);
+      drain_loads();
+      stage_inputs(S, lane, PN);
+    }
+    if (in >= nitems) break;
+    i = in;
+    L = LN;
+    hvn = hvnn;
+  }
+}
+
+// Y of every error-free block from its items' partial sums, added in
+// substream order (fixed, so the result does not depend on which wave ran
+// which item).  One wave per block.
+template <class Acc>
+__global__ void __launch_bounds__(64) k_gemm_finish(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+                                                    GemmArgs ga, const uint32_t* __restrict__ status,
+                                                    ItemScratch is) {
+  const uint32_t lane = lane_id();
+  for (uint32_t b = blockIdx.x; b < nblocks; b += gridDim.x) {
+    const DevBlock d = blocks[b];
+    const uint32_t chunks = is.done[b];
+    if (status[d.status_slot] || !chunks) continue;
+    const float* part = is.partial + (uint64_t)b * kMaxChunks * kMaxItemOut;
+    for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) {
+      float v[kMaxChunks];
+#pragma unroll
+      for (uint32_t k = 0; k < kMaxChunks; ++k) v[k] = k < chunks ? part[k * kMaxItemOut + o] : 0.f;
+      float sum = 0.f;
+#pragma unroll
+      for (uint32_t k = 0; k < kMaxChunks; ++k) sum += v[k];
+      Acc::store(ga, d.dst, o / Acc::kCols, o % Acc::kCols, sum);
+    }
+  }
+}
+
 // Raw blocks: byte copy archive -> output (decode) [src/compile.cpp:466-467].
 __global__ void __launch_bounds__(256) k_copy_raw(const DevBlock* __restrict__ blocks, uint32_t nblocks,
                                                   const uint8_t* __restrict__ arc, uint8_t* __restrict__ out) {
@@ -1571,46 +1696,53 @@ static void gemm_launch(hipStream_t s, const DevBlock* blocks, uint32_t nblocks,
                      codec, arc, ga, status);
 }
 
-// Parallel32 blocks run one workgroup of 4 waves per block (substreams split
-// over the waves), serial blocks one wave per block.
+// Item-scheduled launch (XKSP2 blocks with item scratch): the item kernel
+// over all resident waves, then the in-order reduction.
+template <class Acc>
+static void items_launch(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc,
+                         const GemmArgs& ga, uint32_t* status, const ItemScratch& is, unsigned cus) {
+  static const unsigned per_cu = groups_per_cu(k_gemm_items<Acc>, 64);
+  hipLaunchKernelGGL((k_gemm_items<Acc>), dim3(grid_for((uint64_t)nblocks * kMaxChunks, per_cu * cus)), dim3(64), 0,
+                     s, blocks, nblocks, arc, ga, status, is);
+  hipLaunchKernelGGL((k_gemm_finish<Acc>), dim3(grid_for(nblocks, 8 * cus)), dim3(64), 0, s, blocks, nblocks, ga,
+                     status, is);
+}
+
+// XKSP2 blocks: by substream when item scratch is given, else one workgroup
+// of 4 waves per block (substreams split over the waves).  Serial blocks:
+// one wave per block.
+template <class Acc>
+static void gemm_any(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
+                     const GemmArgs& ga, uint32_t* status, const ItemScratch* is, unsigned cus) {
+  if (codec == kCodecParallel && is) items_launch<Acc>(s, blocks, nblocks, arc, ga, status, *is, cus);
+  else if (codec == kCodecParallel) gemm_launch<4, Acc>(s, blocks, nblocks, codec, arc, ga, status, cus);
+  else gemm_launch<1, Acc>(s, blocks, nblocks, codec, arc, ga, status, cus);
+}
+
 template <template <int> class Acc>
 static void gemm_valu(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
-                      const GemmArgs& ga, uint32_t* status, unsigned cus) {
-  const bool par = codec == kCodecParallel;
-  if (ga.nb == 1) {
-    if (par) gemm_launch<4, Acc<1>>(s, blocks, nblocks, codec, arc, ga, status, cus);
-    else gemm_launch<1, Acc<1>>(s, blocks, nblocks, codec, arc, ga, status, cus);
-  } else if (ga.nb <= 4) {
-    if (par) gemm_launch<4, Acc<4>>(s, blocks, nblocks, codec, arc, ga, status, cus);
-    else gemm_launch<1, Acc<4>>(s, blocks, nblocks, codec, arc, ga, status, cus);
-  } else if (ga.nb <= 8) {
-    if (par) gemm_launch<4, Acc<8>>(s, blocks, nblocks, codec, arc, ga, status, cus);
-    else gemm_launch<1, Acc<8>>(s, blocks, nblocks, codec, arc, ga, status, cus);
-  } else {
-    if (par) gemm_launch<4, Acc<16>>(s, blocks, nblocks, codec, arc, ga, status, cus);
-    else gemm_launch<1, Acc<16>>(s, blocks, nblocks, codec, arc, ga, status, cus);
-  }
+                      const GemmArgs& ga, uint32_t* status, const ItemScratch* is, unsigned cus) {
+  if (ga.nb == 1) gemm_any<Acc<1>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
+  else if (ga.nb <= 4) gemm_any<Acc<4>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
+  else if (ga.nb <= 8) gemm_any<Acc<8>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
+  else gemm_any<Acc<16>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
 }
 
 hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
-                           unsigned cus, hipStream_t s) {
+                           const ItemScratch* is, unsigned cus, hipStream_t s) {
   if (!nblocks) return hipSuccess;
-  gemm_valu<GemmF32>(s, blocks, nblocks, codec, arc, GemmArgs{x, ldx, nb, y, ldy}, status, cus);
+  gemm_valu<GemmF32>(s, blocks, nblocks, codec, arc, GemmArgs{x, ldx, nb, y, ldy}, status, is, cus);
   return hipGetLastError();
 }
 
 hipError_t launch_gemm_bf16(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                             const uint16_t* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, bool mfma,
-                            uint32_t* status, unsigned cus, hipStream_t s) {
+                            uint32_t* status, const ItemScratch* is, unsigned cus, hipStream_t s) {
   if (!nblocks) return hipSuccess;
   const GemmArgs ga{x, ldx, nb, y, ldy};
-  if (mfma && nb >= 8) {
-    if (codec == kCodecParallel) gemm_launch<4, GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, cus);
-    else gemm_launch<1, GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, cus);
-  } else {
-    gemm_valu<GemmBf16>(s, blocks, nblocks, codec, arc, ga, status, cus);
-  }
+  if (mfma && nb >= 8) gemm_any<GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
+  else gemm_valu<GemmBf16>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   return hipGetLastError();
 }
 

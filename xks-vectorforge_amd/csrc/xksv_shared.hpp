@@ -41,5 +41,14 @@ constexpr uint32_t kMaxChunks = 32;
 // Largest batch one fused GEMM launch handles in registers; larger batches
 // are split into column groups by the host.
 constexpr uint32_t kMaxFusedBatch = 16;
+// Fused GEMM over XKSP2 blocks by substream ("items"): per block, kMaxChunks
+// partial-sum slots of kMaxItemOut floats and the block's substream count
+// (written by the item kernel; 0 = header error).
+constexpr uint32_t kMaxItemOut = 16 * kMaxFusedBatch;
+struct ItemScratch {
+  float* partial;  // [blocks][kMaxChunks][kMaxItemOut]
+  uint32_t* done;  // [blocks]
+};
+constexpr uint64_t kItemScratchPerBlock = (uint64_t)kMaxChunks * kMaxItemOut * 4 + 4;
 
 }  // namespace xksv
