@@ -129,3 +129,41 @@ def test_plan_gemv_whole_tensor(hip, codec, shape):
     want = (wt @ x.double()).cpu().numpy()
     got = y.cpu().numpy().astype(np.float64)
     assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-5
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_plan_gemm_reports_corrupt_blocks(hip, batch):
+    """Fused GEMM by substream: a block whose XKSP2 header is damaged (block 1)
+    and one whose substream code bits are damaged (block 3) are reported, their
+    Y rows are left untouched, and every other block's rows are exact."""
+    rows, cols = 96, 4096
+    w = syn.normal_bf16(77 + batch, (rows, cols))
+    enc, table = hip.encode_tensor(w, 2)
+    enc = enc.copy()
+    table = table.copy()
+    table["out_offset"] //= cols * 2
+    t1, t3 = table[1], table[3]
+    enc[t1["offset"]] ^= 0x01                       # magic
+    enc[t3["offset"] + t3["size"] - 3] ^= 0xFF      # code bits of the last substream
+    rc3, _ = hip.try_unpack_parallel(enc[t3["offset"]:t3["offset"] + t3["size"]].tobytes())
+    d_arc = _upload(enc)
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    x = torch.randn(batch, cols, generator=g, device="cuda").to(torch.bfloat16).contiguous()
+    y = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
+    plan.gemm_bf16(d_arc.data_ptr(), x.data_ptr(), batch, y.data_ptr())
+    n, first, bits = plan.errors()
+    assert first == 1 and bits and n == (1 if rc3 == 0 else 2)
+    got = y.cpu().numpy()
+    wt = torch.from_numpy(syn.bf16_to_f32(w).astype(np.float64)).to("cuda")
+    want = (x.double() @ wt.T).cpu().numpy()
+    bad = {1} | ({3} if rc3 else set())
+    for b in range(rows // 16):
+        sl = got[:, 16 * b:16 * b + 16]
+        if b in bad:
+            assert np.isnan(sl).all()
+        else:
+            err = np.linalg.norm(sl - want[:, 16 * b:16 * b + 16]) / np.linalg.norm(want[:, 16 * b:16 * b + 16])
+            assert err <= 1e-5, (b, err)
+    plan.close()

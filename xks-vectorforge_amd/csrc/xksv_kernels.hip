@@ -1266,6 +1266,13 @@ __device__ __forceinline__ uint32_t check_head(uint64_t hv, uint64_t size, const
   return 0;
 }
 
+// Substream starts of a block: lane q (q <= chunks) gets total * q / chunks
+// (the reference's split, cuda/parallel.cu:33-51), one division per lane per
+// block instead of several per substream.
+__device__ __forceinline__ uint32_t substream_starts(uint64_t total, uint32_t chunks, uint32_t lane) {
+  return lane <= chunks && chunks ? (uint32_t)(total * lane / chunks) : 0u;
+}
+
 // The block this wave decodes after `b`.  With a queue (a counter the host
 // zeroes before the launch) the first gridDim.x blocks go one per workgroup and
 // each later one to whichever wave asks first, which balances blocks of
@@ -1305,15 +1312,16 @@ k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
     Writer C{out + d.dst, d.rows, d.cols, (uint32_t)(d.cols / 16), false};
     uint64_t off = 32 + 8ull * chunks;
     uint64_t len = rdlane64(seglen_v, 4);
+    const uint32_t starts = substream_starts(total, chunks, lane);
     StreamIn PN;
-    issue_stream(PN, blk + off, blk + off + len, (uint32_t)(total / chunks), lane);
+    issue_stream(PN, blk + off, blk + off + len, rdlane(starts, 1), lane);
     drain_loads();
     stage_inputs(S, lane, PN);
     for (uint32_t k = 0; k < chunks && !err; ++k) {
-      const uint32_t s0 = (uint32_t)(total * k / chunks), s1 = (uint32_t)(total * (k + 1) / chunks);
+      const uint32_t s0 = rdlane(starts, k), s1 = rdlane(starts, k + 1);
       const uint64_t noff = off + len;
       const uint64_t nlen = k + 1 < chunks ? rdlane64(seglen_v, 4 + k + 1) : 0ull;
-      const uint32_t ncount = k + 1 < chunks ? (uint32_t)(total * (k + 2) / chunks) - s1 : 0u;
+      const uint32_t ncount = k + 1 < chunks ? rdlane(starts, k + 2) - s1 : 0u;
       C.aligned = aligned && unit_aligned(s0, s1 - s0, d.rows, d.cols);
       err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, C,
                        NextStream{k + 1 < chunks ? blk + noff : nullptr, blk + noff + nlen, ncount}, PN);
@@ -1399,15 +1407,15 @@ __global__ void __launch_bounds__(64 * W) k_gemm(const DevBlock* __restrict__ bl
         for (uint32_t q = 0; q < k && q < chunks; ++q) off += rdlane64(hv, 4 + q);
         len = k < chunks ? rdlane64(hv, 4 + k) : 0;
       }
+      const uint32_t starts = substream_starts(total, chunks, lane);
       StreamIn PN;
       if (k < chunks) {
-        issue_stream(PN, blk + off, blk + off + len, (uint32_t)(total * (k + 1) / chunks - total * k / chunks),
-                     lane);
+        issue_stream(PN, blk + off, blk + off + len, rdlane(starts, k + 1) - rdlane(starts, k), lane);
         drain_loads();
         stage_inputs(S, lane, PN);
       }
       for (; k < chunks && !err; k += W) {
-        const uint32_t s0 = (uint32_t)(total * k / chunks), s1 = (uint32_t)(total * (k + 1) / chunks);
+        const uint32_t s0 = rdlane(starts, k), s1 = rdlane(starts, k + 1);
         // next substream of this wave
         uint64_t noff = off, nlen = 0;
         const uint32_t kn = k + W;
@@ -1415,7 +1423,7 @@ __global__ void __launch_bounds__(64 * W) k_gemm(const DevBlock* __restrict__ bl
           for (uint32_t q = k; q < kn; ++q) noff += rdlane64(hv, 4 + q);
           nlen = rdlane64(hv, 4 + kn);
         }
-        const uint32_t ncount = kn < chunks ? (uint32_t)(total * (kn + 1) / chunks - total * kn / chunks) : 0u;
+        const uint32_t ncount = kn < chunks ? rdlane(starts, kn + 1) - rdlane(starts, kn) : 0u;
         if (!Acc::fits(s0, s1 - s0, d.rows, d.cols)) {
           err = kErrShape;
           break;
@@ -1467,8 +1475,9 @@ __device__ __forceinline__ ItemLoc locate_item(const DevBlock& d, const uint8_t*
   const uint64_t incl = wave_incl(len, lane);
   const uint64_t end = 32 + 8ull * L.chunks + rdlane64(incl, 4 + k);
   const uint64_t total = d.rows * d.cols;
-  L.s0 = (uint32_t)(total * k / L.chunks);
-  L.count = (uint32_t)(total * (k + 1) / L.chunks) - L.s0;
+  const uint32_t starts = substream_starts(total, L.chunks, lane);
+  L.s0 = rdlane(starts, k);
+  L.count = rdlane(starts, k + 1) - L.s0;
   L.seg = blk + (end - rdlane64(len, 4 + k));
   L.end = blk + end;
   if (!Acc::fits(L.s0, L.count, d.rows, d.cols)) L.err = kErrShape;
