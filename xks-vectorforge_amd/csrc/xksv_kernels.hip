@@ -72,9 +72,16 @@ struct FastTables {
   uint16_t base[40];             // index of the first length-l symbol in `sorted`
   uint16_t l4[16];               // codes of <= 4 bits, indexed by the top 4 bits
 };
-// The one-symbol table, (len << 8) | symbol, lives in the symbol buffer
-// while the tables are built.
+// The one-symbol table (1,024 words, lut1_entry per code of at most 10
+// bits, kLongMark elsewhere) lives in the symbol buffer while the tables are
+// built.
 constexpr uint32_t kLut1Off = 1024;
+// One-symbol entry: symbol in bits 0-7 and 16-23, length in bits 8-14,
+// 24-27 and 28-31 (the last copy is the shift that skips the code).
+__host__ __device__ constexpr uint32_t lut1_entry(uint32_t len, uint32_t sym) {
+  return sym | (len << 8) | (sym << 16) | (len << 24) | (len << 28);
+}
+static_assert(kLut1Off + 4 * (1u << kLutBits) <= kSymsBytes, "one-symbol table must fit the symbol buffer");
 struct SlowTables {
   uint32_t cnt[256];
   uint16_t base[256];
@@ -338,13 +345,16 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
     }
   }
   wave_sync();
-  uint16_t* lut1 = reinterpret_cast<uint16_t*>(S.syms + kLut1Off);
-  {  // codes of <= 4 bits cover whole 64-entry blocks of the 10-bit LUT
+  uint32_t* lut1 = reinterpret_cast<uint32_t*>(S.syms + kLut1Off);
+  {  // codes of <= 4 bits cover whole 64-entry blocks of the 10-bit table
     const uint32_t e4 = F.l4[lane >> 2];
-    const uint32_t pair = e4 | (e4 << 16);
-    const uint4 v = make_uint4(pair, pair, pair, pair);
-    *reinterpret_cast<uint4*>(&lut1[16 * lane]) = v;
-    *reinterpret_cast<uint4*>(&lut1[16 * lane + 8]) = v;
+    const uint32_t v = e4 ? lut1_entry(e4 >> 8, e4 & 255u) : kLongMark;
+    const uint4 v4 = make_uint4(v, v, v, v);
+    uint4* q = reinterpret_cast<uint4*>(&lut1[16 * lane]);
+    q[0] = v4;
+    q[1] = v4;
+    q[2] = v4;
+    q[3] = v4;
   }
   wave_sync();
   for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
@@ -353,22 +363,26 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
       const uint32_t ent = compact[t], l = ent >> 8, sym = ent & 255u, r = rank[t];
       if (l >= 5 && l <= kLutBits) {  // 2^(10-l) entries, naturally aligned
         const uint64_t code = F.lim[l - 1] + ((uint64_t)r << (32 - l));
-        const uint32_t e0 = (uint32_t)(code >> (32 - kLutBits)), v = (l << 8) | sym, v2 = v | (v << 16);
-        const uint4 v8 = make_uint4(v2, v2, v2, v2);
-        if (l <= 7) {
+        const uint32_t e0 = (uint32_t)(code >> (32 - kLutBits)), v = lut1_entry(l, sym);
+        const uint4 v4 = make_uint4(v, v, v, v);
+        if (l <= 8) {
           uint4* q = reinterpret_cast<uint4*>(&lut1[e0]);
-          q[0] = v8;
-          if (l <= 6) q[1] = v8;
-          if (l == 5) {
-            q[2] = v8;
-            q[3] = v8;
+          q[0] = v4;
+          if (l <= 7) q[1] = v4;
+          if (l <= 6) {
+            q[2] = v4;
+            q[3] = v4;
           }
-        } else if (l == 8) {
-          *reinterpret_cast<uint2*>(&lut1[e0]) = make_uint2(v2, v2);
+          if (l == 5) {
+            q[4] = v4;
+            q[5] = v4;
+            q[6] = v4;
+            q[7] = v4;
+          }
         } else if (l == 9) {
-          *reinterpret_cast<uint32_t*>(&lut1[e0]) = v2;
+          *reinterpret_cast<uint2*>(&lut1[e0]) = make_uint2(v, v);
         } else {
-          lut1[e0] = (uint16_t)v;
+          lut1[e0] = v;
         }
       }
     }
@@ -376,10 +390,14 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
   wave_sync();
   // Two-symbol table: entry e holds its first code and, when the code after
   // it also ends within the 10-bit window, that one too.  Lane l takes
-  // entries l + 64 i, so both the entry reads and the second-code reads
-  // (index (e << l1) mod 1024, consecutive lanes 2^l1 entries apart) spread
-  // over the LDS banks.
-  const uint16_t* lut1r = lut1;
+  // entries l + 64 i (consecutive lanes, consecutive words).  With the
+  // one-symbol entries laid out as lut1_entry, an entry is
+  //   a = first entry & 0x0F007FFF (symbol, length in bits 8-14 and 24-27)
+  //   x = a + (second entry & 0x00FF7F00) (adds the second symbol at bits
+  //       16-23 and its length into bits 8-15: at most 127 + 127)
+  // and holds two codes iff bits 8-15 of x are at most 10; markers (length
+  // 127) never pair.
+  const uint32_t* lut1r = lut1;
 #pragma unroll
   for (uint32_t g = 0; g < 2; ++g) {  // eight entries at a time: two LDS round trips per group
     uint32_t v[8], b[8];
@@ -387,15 +405,12 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
     for (uint32_t i = 0; i < 8; ++i) v[i] = lut1r[lane + kWave * (8 * g + i)];
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i)
-      b[i] = lut1r[((lane + kWave * (8 * g + i)) << (v[i] >> 8)) & ((1u << kLutBits) - 1)];
+      b[i] = lut1r[((lane + kWave * (8 * g + i)) << (v[i] >> 28)) & ((1u << kLutBits) - 1)];
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
-      const uint32_t l1 = v[i] >> 8, l2 = b[i] >> 8;
-      const bool two = v[i] != 0 && b[i] != 0 && l1 + l2 <= kLutBits;
-      F.lut2[lane + kWave * (8 * g + i)] =
-          v[i] == 0 ? kLongMark
-                    : (v[i] & 255u) | ((two ? l1 + l2 : l1) << 8) | (two ? 1u << 15 : 0u) |
-                          (two ? (b[i] & 255u) << 16 : 0u) | (l1 << 24);
+      const uint32_t a = v[i] & 0x0F007FFFu;
+      const uint32_t x = a + (b[i] & 0x00FF7F00u);
+      F.lut2[lane + kWave * (8 * g + i)] = (x & 0xFF00u) <= (kLutBits << 8) ? x | 0x8000u : a;
     }
   }
   wave_sync();
