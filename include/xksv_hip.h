@@ -132,8 +132,10 @@ int xksv_hip_plan_destroy(xksv_hip_plan* plan);
 int xksv_hip_plan_decode(xksv_hip_plan* plan, const void* archive, void* out, uint64_t out_size, void* stream);
 
 /* Enqueue fused decode-GEMM, fp32 X [cols, batch] row-major, Y [rows, batch]
- * (block rows start at out_offset).  All blocks must share `cols`.  batch = 1
- * is the batch-1 GEMV of python/runtime.py:264-284. */
+ * (block rows start at out_offset).  All blocks must share `cols`; raw blocks
+ * (rows = cols = 0 in archive indexes) take it from the compressed ones, and a
+ * table of raw blocks only must give it in their cols field.  batch = 1 is the
+ * batch-1 GEMV of python/runtime.py:264-284. */
 int xksv_hip_plan_gemm(xksv_hip_plan* plan, const void* archive, const float* x, size_t batch, float* y,
                        void* stream);
 

@@ -301,6 +301,9 @@ bool prepare_gemm(xksv_hip_plan* P) {
   uint64_t cols = 0;
   for (const auto& b : P->blocks)
     if (b.codec != XKSV_CODEC_RAW) cols = b.cols;
+  if (!cols)  // raw blocks only: the row width comes from their cols field (0 in archive indexes)
+    for (const auto& b : P->blocks)
+      if (b.cols) cols = b.cols;
   if (!cols) return false;
   std::vector<DevBlock> fs, fp, gds, gdp, gp, raw;
   uint64_t scratch = 0, rows_extent = 0;
