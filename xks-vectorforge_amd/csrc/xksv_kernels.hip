@@ -180,18 +180,18 @@ struct Fetch16 {
   uint4 v;
   uint32_t drop;  // leading bytes to drop; 16 = none of the bytes are wanted
   __device__ __forceinline__ uint4 value() const {
-    const uint32_t d = drop >> 2, r = drop & 3u;
-    const uint32_t w[5] = {v.x, v.y, v.z, v.w, 0u};
-    uint32_t o[4];
-#pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-      const uint32_t lo = d == 0 ? w[k] : d == 1 ? w[k + 1 < 5 ? k + 1 : 4] : d == 2 ? w[k + 2 < 5 ? k + 2 : 4]
-                                                  : d == 3 ? w[k + 3 < 5 ? k + 3 : 4] : 0u;
-      const uint32_t hi = d == 0 ? w[k + 1 < 5 ? k + 1 : 4] : d == 1 ? w[k + 2 < 5 ? k + 2 : 4]
-                                                            : d == 2 ? w[k + 3 < 5 ? k + 3 : 4] : 0u;
-      o[k] = r ? __builtin_amdgcn_alignbyte(hi, lo, r) : lo;
+    // The 16 bytes as a 128-bit little-endian value shifted right by 8 drop bits.
+    const uint32_t sh = 8u * drop;
+    const uint64_t lo = (uint64_t)v.x | ((uint64_t)v.y << 32), hi = (uint64_t)v.z | ((uint64_t)v.w << 32);
+    uint64_t olo, ohi;
+    if (sh >= 64) {
+      olo = sh >= 128 ? 0ull : hi >> (sh - 64);
+      ohi = 0ull;
+    } else {
+      olo = sh ? (lo >> sh) | (hi << (64 - sh)) : lo;
+      ohi = hi >> sh;
     }
-    return make_uint4(o[0], o[1], o[2], o[3]);
+    return make_uint4((uint32_t)olo, (uint32_t)(olo >> 32), (uint32_t)ohi, (uint32_t)(ohi >> 32));
   }
 };
 __device__ __forceinline__ Fetch16 fetch16(const uint8_t* p, const uint8_t* end) {
@@ -785,32 +785,44 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
 #pragma unroll
       for (uint32_t q = kQ; q < kQ + 4; ++q) R[q] = 0u;
       wave_sync();
-      uint32_t* d32 = reinterpret_cast<uint32_t*>(S.syms + (dst & ~3u));
-      const uint32_t sh = (4u - dh) & 3u;  // destination dword k = run bytes [4k - dh, 4k - dh + 4)
-      const uint32_t nw = (dh + t) >> 2;   // destination dwords that end inside the run
-      uint32_t head = 0, tail = 0;
+      const uint32_t nw = (dh + t) >> 2;  // destination dwords that end inside the run
+      // Destination dword k = run bytes [4k - dh, 4k - dh + 4): bytes 4 - dh
+      // .. 7 of source dwords k - 1, k (one byte permute).  Whole dwords are written
+      // without per-dword predicates: a lane writes dwords 0 .. (its block of
+      // nqmax) + 3, highest first.  Past its run they hold garbage, which
+      // lands only on later lanes' dwords of lower index k' < k -- written
+      // after it in this order -- or past the data.  A lane whose run starts
+      // and ends inside one dword (nw == 0) could share its base dword with
+      // the next lane, so it writes to kDummy instead.  A run's first dword,
+      // when shared with the bytes before it (dh != 0), is left to byte
+      // stores; its last dword (bytes 0 .. (dh + t) % 4 - 1 of dword nw) is
+      // written whole at step nw and no later store covers those bytes: the
+      // next run writes that dword only when it starts aligned, i.e. when no
+      // byte of this run is in it.
+      constexpr uint32_t kDummy = kSymsBytes - 4 * (kQ + 4);
+      static_assert(255 + kSegBits + 4 * (kQ + 4) <= kDummy, "compaction garbage must stay off the dummy run");
+      uint32_t* d32 = reinterpret_cast<uint32_t*>(S.syms + (nw ? (dst & ~3u) : kDummy));
+      const uint32_t sel = 0x07060504u - 0x01010101u * dh;  // byte selector of (R[k], R[k - 1])
+      uint32_t head = 0;
 #pragma unroll
-      for (uint32_t k0 = 0; k0 <= kQ; k0 += 4) {
-        if (k0 <= nqmax) {
+      for (int k0 = (int)kQ; k0 >= 0; k0 -= 4) {
+        if ((uint32_t)k0 <= nqmax) {
 #pragma unroll
-          for (uint32_t k = k0; k < k0 + 4; ++k) {
-            const uint32_t cur = R[k], prev = k ? R[k - 1] : 0u;
-            const uint32_t w = dh ? __builtin_amdgcn_alignbyte(cur, prev, sh) : cur;
+          for (int k = k0 + 3; k >= k0; --k) {
+            const uint32_t w = __builtin_amdgcn_perm(R[k], k ? R[k - 1] : 0u, sel);
             if (k == 0) head = w;
-            tail = k == nw ? w : tail;
-            if (k < nw && (k > 0 || dh == 0)) d32[k] = w;
+            if (k > 0 || dh == 0) d32[k] = w;
+            wave_sync();  // keeps the stores one dword per instruction, in this order
           }
         }
       }
+      // Bytes of the first dword when it is shared (dh != 0) or holds the
+      // whole run (nw == 0).
       lds_bytes d8 = as_lds(S.syms + (dst & ~3u));
-      // Head: bytes dh..3 of dword 0 (when the run does not start aligned).
+      const bool first_bytes = dh != 0 || nw == 0;
 #pragma unroll
-      for (uint32_t b = 1; b < 4; ++b)
-        if (dh && b >= dh && b - dh < t) d8[b] = (uint8_t)(head >> (8 * b));
-      // Tail: bytes 0..(dh + t) % 4 - 1 of dword nw, unless that is the head dword.
-#pragma unroll
-      for (uint32_t b = 0; b < 3; ++b)
-        if ((nw > 0 || dh == 0) && b < ((dh + t) & 3u)) d8[4 * nw + b] = (uint8_t)(tail >> (8 * b));
+      for (uint32_t b = 0; b < 4; ++b)
+        if (first_bytes && b >= dh && b - dh < t) d8[b] = (uint8_t)(head >> (8 * b));
       wave_sync();
     }
     const uint32_t avail = carry + total;
