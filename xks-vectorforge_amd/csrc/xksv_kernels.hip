@@ -489,17 +489,18 @@ struct Path {
 };
 constexpr uint32_t kNoStart = 0xffffffffu;
 
-// Slide the register window (w0, w1, w2 = segment dwords wi - 1 .. wi + 1,
-// wi = (p + 31) / 32) after p advanced by at most 32 bits; the third dword is
-// re-read from LDS off the dependency chain.
-__device__ __forceinline__ void slide(const Smem& S, uint32_t p, uint32_t& wi, uint32_t& w0, uint32_t& w1,
+// The register window: w0, w1, w2 = segment dwords j - 1 .. j + 1 with
+// j = ceil(p / 32), and wb = 32 j, the first bit past w0.  Slide it after p
+// advanced by at most 32 bits (p > wb: p left w0); the third dword is re-read
+// from LDS off the dependency chain.
+__device__ __forceinline__ void slide(const Smem& S, uint32_t p, uint32_t& wb, uint32_t& w0, uint32_t& w1,
                                       uint32_t& w2) {
-  const uint32_t i1 = (p + 31) >> 5;
-  const bool adv = i1 != wi;
-  wi = i1;
+  const bool adv = p > wb;
+  wb += adv ? 32u : 0u;
+  __builtin_assume((wb & 31u) == 0u);
   w0 = adv ? w1 : w0;
   w1 = adv ? w2 : w1;
-  w2 = S.stream[i1 + 2];
+  w2 = S.stream[(wb >> 5) + 2];
 }
 
 // Up to two codewords at bit p (lut2 entry layout).  A window without a code
@@ -529,12 +530,13 @@ __device__ __forceinline__ uint32_t end_pair(uint32_t le, uint32_t end, uint32_t
   return back;
 }
 
-__device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t& wi, uint32_t& w0, uint32_t& w1,
+__device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t& wb, uint32_t& w0, uint32_t& w1,
                                             uint32_t& w2) {
-  wi = (p + 31) >> 5;
-  w0 = S.stream[wi];
-  w1 = S.stream[wi + 1];
-  w2 = S.stream[wi + 2];
+  const uint32_t j = (p + 31) >> 5;
+  wb = 32u * j;
+  w0 = S.stream[j];
+  w1 = S.stream[j + 1];
+  w2 = S.stream[j + 2];
 }
 
 // The last step's entry `le` was kLongMark: move p back to that step's start
