@@ -1007,10 +1007,26 @@ struct Writer {
     }
     const uint32_t take = final ? avail : (avail & ~255u);
     const uint32_t units = take >> 3;
+    if (rows == 16) {
+      // One band: unit lane + 64 i is two tiles (64 bytes of its row) after
+      // unit lane + 64 (i - 1), so one address serves the window.
+      const uint32_t U = ((st.start + pos0) >> 3) + lane;
+      uint8_t* const p = out + 2ull * (((U >> 1) & 15u) * (uint32_t)cols + 16u * (U >> 5) + 8u * (U & 1u));
 #pragma unroll
-    for (uint32_t i = 0; i < kSmWin; ++i) {
-      const uint32_t u = lane + kWave * i;
-      if (u < units) unit(S, st, pos0, u, W.v[i]);
+      for (uint32_t i = 0; i < kSmWin; ++i) {
+        if (lane + kWave * i < units) {
+          uint64_t E;
+          __builtin_memcpy(&E, S.syms + 8 * (lane + kWave * i), 8);
+          const uint4 w = combine8(E, W.v[i]);
+          __builtin_memcpy(p + 64 * i, &w, 16);
+        }
+      }
+    } else {
+#pragma unroll
+      for (uint32_t i = 0; i < kSmWin; ++i) {
+        const uint32_t u = lane + kWave * i;
+        if (u < units) unit(S, st, pos0, u, W.v[i]);
+      }
     }
     for (uint32_t u = lane + kSmWin * kWave; u < units; u += kWave)
       unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
