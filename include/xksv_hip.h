@@ -145,6 +145,16 @@ int xksv_hip_plan_gemm(xksv_hip_plan* plan, const void* archive, const float* x,
 int xksv_hip_plan_gemm_bf16(xksv_hip_plan* plan, const void* archive, const uint16_t* x, size_t batch, float* y,
                             void* stream);
 
+/* No reference counterpart as a C entry (the reference hashes on the host,
+ * src/verify.cpp:262-273): enqueue SHA-256 of every block's decoded bytes --
+ * out[out_offset, out_offset + raw_size), as written by xksv_hip_plan_decode
+ * into `out` (device, out_size bytes) on the same stream -- into `digests`
+ * (device, digests_size >= 32 bytes per block, in table order: the per-slab
+ * digests of src/compile.cpp:255,443,489).  0 on success, 1 on error (null
+ * pointers or buffers too small for the plan). */
+int xksv_hip_plan_digests(xksv_hip_plan* plan, const void* out, uint64_t out_size, uint8_t* digests,
+                          uint64_t digests_size, void* stream);
+
 /* Synchronize `stream`, return the number of failed blocks (or -1 on a HIP
  * error); *first_bad (optional) gets the first failing block index or -1,
  * *bits (optional) the OR of all error bits. */

@@ -598,6 +598,18 @@ int xksv_hip_plan_gemm_bf16(xksv_hip_plan* P, const void* archive, const uint16_
   return plan_gemm(P, archive, x, batch, y, stream, true);
 }
 
+int xksv_hip_plan_digests(xksv_hip_plan* P, const void* out, uint64_t out_size, uint8_t* digests,
+                          uint64_t digests_size, void* stream) {
+  if (!P || !out || !digests || out_size < P->out_extent || digests_size < 32ull * P->blocks.size()) return 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint8_t* o = static_cast<const uint8_t*>(out);
+  return launch_sha256_blocks(P->d_serial, P->n_serial, o, digests, s) != hipSuccess ||
+                 launch_sha256_blocks(P->d_parallel, P->n_parallel, o, digests, s) != hipSuccess ||
+                 launch_sha256_blocks(P->d_raw, P->n_raw, o, digests, s) != hipSuccess
+             ? 1
+             : 0;
+}
+
 int64_t xksv_hip_plan_errors(xksv_hip_plan* P, void* stream, int64_t* first_bad, uint32_t* bits) {
   if (first_bad) *first_bad = -1;
   if (bits) *bits = 0;

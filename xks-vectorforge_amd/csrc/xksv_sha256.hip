@@ -1,0 +1,143 @@
+// SHA-256 (FIPS 180-4) of each block's decoded bytes, on the GPU: the
+// per-slab digests an archive index records for the original-order bytes of
+// every block [src/compile.cpp:255,443,489], which verification compares
+// after decoding [src/verify.cpp:262-273].
+//
+// One lane per block: SHA-256 is sequential within a message, and an archive
+// has tens of thousands of blocks, so lanes hash independent blocks side by
+// side.  The 64 rounds are unrolled with the round constants as immediates;
+// the message schedule is a rolling 16-word window in registers.  A lane
+// reads its block 64 bytes at a time (four 16-byte loads when the block is
+// 16-byte aligned, as every slab of a decoded tensor is; byte loads
+// otherwise).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "xksv_shared.hpp"
+
+namespace xksv {
+namespace {
+
+constexpr uint32_t kSha256K[64] = {
+    0x428a2f98u, 0x71374491u, 0xb5c0fbcfu, 0xe9b5dba5u, 0x3956c25bu, 0x59f111f1u, 0x923f82a4u, 0xab1c5ed5u,
+    0xd807aa98u, 0x12835b01u, 0x243185beu, 0x550c7dc3u, 0x72be5d74u, 0x80deb1feu, 0x9bdc06a7u, 0xc19bf174u,
+    0xe49b69c1u, 0xefbe4786u, 0x0fc19dc6u, 0x240ca1ccu, 0x2de92c6fu, 0x4a7484aau, 0x5cb0a9dcu, 0x76f988dau,
+    0x983e5152u, 0xa831c66du, 0xb00327c8u, 0xbf597fc7u, 0xc6e00bf3u, 0xd5a79147u, 0x06ca6351u, 0x14292967u,
+    0x27b70a85u, 0x2e1b2138u, 0x4d2c6dfcu, 0x53380d13u, 0x650a7354u, 0x766a0abbu, 0x81c2c92eu, 0x92722c85u,
+    0xa2bfe8a1u, 0xa81a664bu, 0xc24b8b70u, 0xc76c51a3u, 0xd192e819u, 0xd6990624u, 0xf40e3585u, 0x106aa070u,
+    0x19a4c116u, 0x1e376c08u, 0x2748774cu, 0x34b0bcb5u, 0x391c0cb3u, 0x4ed8aa4au, 0x5b9cca4fu, 0x682e6ff3u,
+    0x748f82eeu, 0x78a5636fu, 0x84c87814u, 0x8cc70208u, 0x90befffau, 0xa4506cebu, 0xbef9a3f7u, 0xc67178f2u};
+
+__device__ __forceinline__ uint32_t rotr(uint32_t x, uint32_t n) { return __builtin_amdgcn_alignbit(x, x, n); }
+__device__ __forceinline__ uint32_t be32(uint32_t v) { return __builtin_amdgcn_perm(0u, v, 0x00010203u); }
+
+// One 64-byte chunk (16 big-endian words) into the state.
+__device__ __forceinline__ void compress(uint32_t (&h)[8], uint32_t (&w)[16]) {
+  uint32_t a = h[0], b = h[1], c = h[2], d = h[3], e = h[4], f = h[5], g = h[6], k = h[7];
+#pragma unroll
+  for (int t = 0; t < 64; ++t) {
+    uint32_t wt;
+    if (t < 16) {
+      wt = w[t];
+    } else {
+      const uint32_t w15 = w[(t - 15) & 15], w2 = w[(t - 2) & 15];
+      const uint32_t s0 = rotr(w15, 7) ^ rotr(w15, 18) ^ (w15 >> 3);
+      const uint32_t s1 = rotr(w2, 17) ^ rotr(w2, 19) ^ (w2 >> 10);
+      wt = w[t & 15] + s0 + w[(t - 7) & 15] + s1;
+      w[t & 15] = wt;
+    }
+    const uint32_t S1 = rotr(e, 6) ^ rotr(e, 11) ^ rotr(e, 25);
+    const uint32_t ch = (e & f) ^ (~e & g);
+    const uint32_t t1 = k + S1 + ch + kSha256K[t] + wt;
+    const uint32_t S0 = rotr(a, 2) ^ rotr(a, 13) ^ rotr(a, 22);
+    const uint32_t mj = (a & b) ^ (a & c) ^ (b & c);
+    k = g;
+    g = f;
+    f = e;
+    e = d + t1;
+    d = c;
+    c = b;
+    b = a;
+    a = t1 + S0 + mj;
+  }
+  h[0] += a;
+  h[1] += b;
+  h[2] += c;
+  h[3] += d;
+  h[4] += e;
+  h[5] += f;
+  h[6] += g;
+  h[7] += k;
+}
+
+// Block b's decoded bytes: out[dst, dst + raw bytes); digest into
+// digests[32 * status_slot].
+__global__ void __launch_bounds__(256) k_sha256_blocks(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+                                                       const uint8_t* __restrict__ out, uint8_t* __restrict__ digests) {
+  const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  const DevBlock d = blocks[b];
+  const uint64_t n = d.codec == kCodecRaw ? d.size : d.rows * d.cols * 2;
+  const uint8_t* p = out + d.dst;
+  uint32_t h[8] = {0x6a09e667u, 0xbb67ae85u, 0x3c6ef372u, 0xa54ff53au,
+                   0x510e527fu, 0x9b05688cu, 0x1f83d9abu, 0x5be0cd19u};
+  uint32_t w[16];
+  const uint64_t full = n / 64;
+  const bool aligned = (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+  for (uint64_t c = 0; c < full; ++c) {
+    const uint8_t* q = p + 64 * c;
+    if (aligned) {
+      const uint4* q4 = reinterpret_cast<const uint4*>(q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = q4[i];
+        w[4 * i] = be32(v.x);
+        w[4 * i + 1] = be32(v.y);
+        w[4 * i + 2] = be32(v.z);
+        w[4 * i + 3] = be32(v.w);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        w[i] = ((uint32_t)q[4 * i] << 24) | ((uint32_t)q[4 * i + 1] << 16) | ((uint32_t)q[4 * i + 2] << 8) | q[4 * i + 3];
+    }
+    compress(h, w);
+  }
+  // Padding: the r remaining bytes, 0x80, zeros, then the bit length
+  // (big-endian 64-bit) in the last 8 bytes; two chunks when r >= 56.
+  const uint32_t r = (uint32_t)(n % 64);
+  const uint8_t* q = p + 64 * full;
+  const uint64_t bits = n * 8;
+  for (uint32_t chunk = 0; chunk < (r >= 56 ? 2u : 1u); ++chunk) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t at = 64 * chunk + 4 * i + j;
+        const uint32_t byte = at < r ? q[at] : at == r ? 0x80u : 0u;
+        word = (word << 8) | byte;
+      }
+      w[i] = word;
+    }
+    if (chunk == (r >= 56 ? 1u : 0u)) {
+      w[14] = (uint32_t)(bits >> 32);
+      w[15] = (uint32_t)bits;
+    }
+    compress(h, w);
+  }
+  uint32_t* dg = reinterpret_cast<uint32_t*>(digests + 32ull * d.status_slot);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dg[i] = be32(h[i]);
+}
+
+}  // namespace
+
+hipError_t launch_sha256_blocks(const DevBlock* blocks, uint32_t nblocks, const uint8_t* out, uint8_t* digests,
+                                hipStream_t s) {
+  if (!nblocks) return hipSuccess;
+  hipLaunchKernelGGL(k_sha256_blocks, dim3((nblocks + 255) / 256), dim3(256), 0, s, blocks, nblocks, out, digests);
+  return hipGetLastError();
+}
+
+}  // namespace xksv

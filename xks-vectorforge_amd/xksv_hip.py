@@ -64,6 +64,7 @@ _SIGNATURES = {
     "xksv_hip_plan_gemm": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "xksv_hip_plan_gemm_bf16": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "xksv_hip_plan_errors": (ctypes.c_int64, [_vp, _vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(_u32)]),
+    "xksv_hip_plan_digests": (ctypes.c_int, [_vp, _vp, _u64, _vp, _u64, _vp]),
     "xksv_encode_tensor": (_int, [_vp, _u64, _int, _u64, _u32, _u32, _pvp, ctypes.POINTER(_u64),
                                   ctypes.POINTER(ctypes.POINTER(Block)), ctypes.POINTER(_u64)]),
     "xksv_hip_version": (_int, []),
@@ -210,6 +211,13 @@ class Plan:
         """bf16 X [batch, cols] -> fp32 Y [batch, M] (layout of x @ W.T)."""
         if self.lib.lib.xksv_hip_plan_gemm_bf16(self.handle, archive_ptr, x_ptr, batch, y_ptr, stream or None):
             raise XksvError("xksv_hip_plan_gemm_bf16 failed to launch")
+
+    def digests(self, out_ptr: int, out_size: int, digests_ptr: int, digests_size: int, stream: int = 0) -> None:
+        """SHA-256 of every block's decoded bytes in `out` (device) into
+        `digests` (device, 32 bytes per block in table order)."""
+        if self.lib.lib.xksv_hip_plan_digests(self.handle, out_ptr, out_size, digests_ptr, digests_size,
+                                              stream or None):
+            raise XksvError("xksv_hip_plan_digests failed to launch")
 
     def errors(self, stream: int = 0):
         """(number of failed blocks, first failing block or -1, OR of error bits)."""
