@@ -65,10 +65,13 @@ def build_archive(torch, lib, layers: int, codec: int):
     encs, tables, meta = [], [], []
     arc_off = out_off = 0
     t0 = time.time()
+    t_enc = 0.0
     for idx, (name, shape) in enumerate(tensors):
         w = gen_bf16(torch, shape, 1000 + idx, name.endswith("norm"))
         words = w.view(torch.int16).cpu().numpy().view(np.uint16)
+        te = time.perf_counter()
         enc, table = lib.encode_tensor(words, codec)
+        t_enc += time.perf_counter() - te
         table = table.copy()
         table["offset"] += arc_off
         table["out_offset"] += out_off
@@ -80,6 +83,8 @@ def build_archive(torch, lib, layers: int, codec: int):
         if idx % 40 == 0:
             log(f"encoded {idx + 1}/{len(tensors)} tensors, {out_off / 1e9:.1f} GB raw, {time.time() - t0:.0f}s")
     table = np.concatenate(tables)
+    build_archive.encode = {"seconds": round(t_enc, 3), "raw_gbps": round(out_off / t_enc / 1e9, 3),
+                            "threads": os.cpu_count()}
     d_arc = torch.empty(arc_off, dtype=torch.uint8, device="cuda")
     pos = 0
     for e in encs:
@@ -404,6 +409,7 @@ def main() -> int:
         "decode_4096x4096_serial": c1, "decode_mixed_archive": c3,
         "hbm_copy_gbps": round(copy_gbps, 1),
         "slab_sha256_gpu": dg,
+        "host_encoder": build_archive.encode,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 
 import xksv_hip
+import xksv_synth as syn
 from conftest import GOLDEN, PKG, ROOT
 from oracle_lib import gen, raw_bytes, sha
 
@@ -107,3 +108,14 @@ def test_kernels_address_lds_without_flat_instructions(tmp_path):
     assert "_ZN4xksv12_GLOBAL__N_117k_decode_parallel" in text
     scratch = re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text)
     assert scratch and all(int(s) == 0 for s in scratch)
+
+
+@pytest.mark.parametrize("codec", [1, 2])
+def test_encode_tensor_worker_count_determinism(hip, codec):
+    """Encoded bytes and block table do not depend on the worker count
+    (tests/test_inspect.cpp:77-85 pins the same for the compiler's Workers)."""
+    w = syn.normal_bf16(31 + codec, (200, 4096))
+    ref_enc, ref_table = hip.encode_tensor(w, codec, threads=1)
+    for threads in (2, 3, 8):
+        enc, table = hip.encode_tensor(w, codec, threads=threads)
+        assert enc.tobytes() == ref_enc.tobytes() and table.tobytes() == ref_table.tobytes()
