@@ -329,11 +329,17 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
   if (lane < 16) F.l4[lane] = 0;
   if (total > (1ull << 32)) return Book{kErrCodebook, maxlen, true};
   wave_sync();
+  uint32_t rl = 0, rs = 0, re0 = 0;  // this lane's code of the first round (t = lane): length, symbol, 10-bit start
   for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
     const uint32_t t = s0 + lane;
     if (t < m) {
       const uint32_t ent = compact[t], l = ent >> 8, sym = ent & 255u, r = rank[t];
       const uint64_t code = F.lim[l - 1] + ((uint64_t)r << (32 - l));
+      if (s0 == 0) {
+        rl = l;
+        rs = sym;
+        re0 = (uint32_t)(code >> (32 - kLutBits));
+      }
       S.sorted[F.base[l] + r] = (uint8_t)sym;
       if (l <= 4) {  // 2^(4-l) entries, naturally aligned
         const uint32_t e0 = (uint32_t)(code >> 28), v = (l << 8) | sym, v2 = v | (v << 16);
@@ -357,33 +363,39 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
     q[3] = v4;
   }
   wave_sync();
-  for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
-    const uint32_t t = s0 + lane;
-    if (t < m) {
-      const uint32_t ent = compact[t], l = ent >> 8, sym = ent & 255u, r = rank[t];
-      if (l >= 5 && l <= kLutBits) {  // 2^(10-l) entries, naturally aligned
-        const uint64_t code = F.lim[l - 1] + ((uint64_t)r << (32 - l));
-        const uint32_t e0 = (uint32_t)(code >> (32 - kLutBits)), v = lut1_entry(l, sym);
-        const uint4 v4 = make_uint4(v, v, v, v);
-        if (l <= 8) {
-          uint4* q = reinterpret_cast<uint4*>(&lut1[e0]);
-          q[0] = v4;
-          if (l <= 7) q[1] = v4;
-          if (l <= 6) {
-            q[2] = v4;
-            q[3] = v4;
-          }
-          if (l == 5) {
-            q[4] = v4;
-            q[5] = v4;
-            q[6] = v4;
-            q[7] = v4;
-          }
-        } else if (l == 9) {
-          *reinterpret_cast<uint2*>(&lut1[e0]) = make_uint2(v, v);
-        } else {
-          lut1[e0] = v;
-        }
+  // Codes of 5..10 bits: 2^(10-l) entries from e0, naturally aligned.
+  const auto range_fill = [&](uint32_t l, uint32_t sym, uint32_t e0) {
+    const uint32_t v = lut1_entry(l, sym);
+    const uint4 v4 = make_uint4(v, v, v, v);
+    if (l <= 8) {
+      uint4* q = reinterpret_cast<uint4*>(&lut1[e0]);
+      q[0] = v4;
+      if (l <= 7) q[1] = v4;
+      if (l <= 6) {
+        q[2] = v4;
+        q[3] = v4;
+      }
+      if (l == 5) {
+        q[4] = v4;
+        q[5] = v4;
+        q[6] = v4;
+        q[7] = v4;
+      }
+    } else if (l == 9) {
+      *reinterpret_cast<uint2*>(&lut1[e0]) = make_uint2(v, v);
+    } else {
+      lut1[e0] = v;
+    }
+  };
+  if (m <= kWave) {  // one symbol per lane: its code is still in registers
+    if (lane < m && rl >= 5 && rl <= kLutBits) range_fill(rl, rs, re0);
+  } else {
+    for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
+      const uint32_t t = s0 + lane;
+      if (t < m) {
+        const uint32_t ent = compact[t], l = ent >> 8, sym = ent & 255u, r = rank[t];
+        if (l >= 5 && l <= kLutBits)
+          range_fill(l, sym, (uint32_t)((F.lim[l - 1] + ((uint64_t)r << (32 - l))) >> (32 - kLutBits)));
       }
     }
   }
