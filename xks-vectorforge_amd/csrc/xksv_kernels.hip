@@ -299,21 +299,37 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
   if (L2) compact[k++] = (uint16_t)((L2 << 8) | (4 * lane + 2));
   if (L3) compact[k++] = (uint16_t)((L3 << 8) | (4 * lane + 3));
   if (lane < 40) F.cnt[lane] = 0;
-  for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
-    const uint32_t t = s0 + lane;
-    const bool valid = t < m;
+  // One symbol per lane (m <= 64, the usual case): its entry and rank stay in
+  // registers for the passes below.
+  uint32_t ent0 = 0, r0 = 0;
+  if (m <= kWave) {
+    const bool valid = lane < m;
     if (lane < 40) F.slots[lane] = 0;
     wave_sync();
-    const uint32_t ent = valid ? compact[t] : 0u;
-    const uint32_t l = ent >> 8;
+    ent0 = valid ? compact[lane] : 0u;
+    const uint32_t l = ent0 >> 8;
     if (valid) atomicOr(reinterpret_cast<unsigned long long*>(&F.slots[l]), 1ull << lane);
     wave_sync();
     const uint64_t mk = valid ? F.slots[l] : 0ull;
-    const uint32_t rin = mbcnt(mk);
-    const uint32_t r = valid ? rin + F.cnt[l] : 0u;
-    wave_sync();
-    if (valid && rin == 0) F.cnt[l] += (uint32_t)__popcll(mk);
-    if (valid) rank[t] = (uint8_t)r;
+    r0 = valid ? mbcnt(mk) : 0u;
+    if (valid && r0 == 0) F.cnt[l] = (uint32_t)__popcll(mk);
+  } else {
+    for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
+      const uint32_t t = s0 + lane;
+      const bool valid = t < m;
+      if (lane < 40) F.slots[lane] = 0;
+      wave_sync();
+      const uint32_t ent = valid ? compact[t] : 0u;
+      const uint32_t l = ent >> 8;
+      if (valid) atomicOr(reinterpret_cast<unsigned long long*>(&F.slots[l]), 1ull << lane);
+      wave_sync();
+      const uint64_t mk = valid ? F.slots[l] : 0ull;
+      const uint32_t rin = mbcnt(mk);
+      const uint32_t r = valid ? rin + F.cnt[l] : 0u;
+      wave_sync();
+      if (valid && rin == 0) F.cnt[l] += (uint32_t)__popcll(mk);
+      if (valid) rank[t] = (uint8_t)r;
+    }
   }
   wave_sync();
   // Per-length group sums: C(l+1) = sum_{l' <= l} cnt[l'] * 2^(32 - l').
@@ -333,7 +349,8 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
   for (uint32_t s0 = 0; s0 < m; s0 += kWave) {
     const uint32_t t = s0 + lane;
     if (t < m) {
-      const uint32_t ent = compact[t], l = ent >> 8, sym = ent & 255u, r = rank[t];
+      const bool one = m <= kWave;
+      const uint32_t ent = one ? ent0 : compact[t], l = ent >> 8, sym = ent & 255u, r = one ? r0 : rank[t];
       const uint64_t code = F.lim[l - 1] + ((uint64_t)r << (32 - l));
       if (s0 == 0) {
         rl = l;
