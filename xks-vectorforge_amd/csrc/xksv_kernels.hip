@@ -426,15 +426,27 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
   //       16-23 and its length into bits 8-15: at most 127 + 127)
   // and holds two codes iff bits 8-15 of x are at most 10; markers (length
   // 127) never pair.
+  //
+  // The second entry is read at the window shifted past the first code, whose
+  // low l1 bits would be padding zeros.  Any fill of those bits gives the
+  // same result: a second code that fits the window lies wholly in the shifted
+  // bits, and one that does not fit is rejected whatever the entry read.  The
+  // fill is the lane's top bits (lane << l1 >> 6), so that lanes read distinct
+  // LDS banks instead of the 2^l1-way conflict of the zero-padded addresses;
+  // for a marker (l1 = 0) the fill lands above bit 9 and is masked off.
   const uint32_t* lut1r = lut1;
+  const uint32_t lane_hi = lane << 26;
 #pragma unroll
   for (uint32_t g = 0; g < 2; ++g) {  // eight entries at a time: two LDS round trips per group
     uint32_t v[8], b[8];
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) v[i] = lut1r[lane + kWave * (8 * g + i)];
 #pragma unroll
-    for (uint32_t i = 0; i < 8; ++i)
-      b[i] = lut1r[((lane + kWave * (8 * g + i)) << (v[i] >> 28)) & ((1u << kLutBits) - 1)];
+    for (uint32_t i = 0; i < 8; ++i) {
+      const uint32_t l1 = v[i] >> 28;
+      const uint32_t fill = __builtin_amdgcn_alignbit(0u, lane_hi, 32u - l1);
+      b[i] = lut1r[(((lane + kWave * (8 * g + i)) << l1) | fill) & ((1u << kLutBits) - 1)];
+    }
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
       const uint32_t a = v[i] & 0x0F007FFFu;
