@@ -374,10 +374,10 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
     const uint32_t v = e4 ? lut1_entry(e4 >> 8, e4 & 255u) : kLongMark;
     const uint4 v4 = make_uint4(v, v, v, v);
     uint4* q = reinterpret_cast<uint4*>(&lut1[16 * lane]);
-    q[0] = v4;
-    q[1] = v4;
-    q[2] = v4;
-    q[3] = v4;
+    // Lane l writes its 16 words in an order rotated by l >> 2, so each
+    // store of 16 lanes covers all 64 LDS banks once.
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) q[(j + (lane >> 2)) & 3] = v4;
   }
   wave_sync();
   // Codes of 5..10 bits: 2^(10-l) entries from e0, naturally aligned.
