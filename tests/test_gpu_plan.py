@@ -75,7 +75,6 @@ def test_config3_mixed_archive(hip, codec):
     t = t.copy(); t["offset"] += base; t["out_offset"] += obase
     encs.append(e); tables.append(t); raws.append(fp32.tobytes())
     enc, table = np.concatenate(encs), np.concatenate(tables)
-    assert (table["codec"][-2] == 0) or codec == 1 or True
     d_arc = _upload(enc)
     total = sum(len(r) for r in raws)
     out = torch.zeros(total, dtype=torch.uint8, device="cuda")
@@ -88,21 +87,32 @@ def test_config3_mixed_archive(hip, codec):
     assert set(uni["codec"]) == {0}
 
 
-def test_plan_reports_corrupt_blocks(hip):
+def _corrupt_code_bits(oracle, enc, t) -> None:
+    """Flip one byte of the last substream's code bits of block `t` in place, choosing
+    (deterministically, nearest the end first) a byte whose flip the oracle rejects."""
+    end = int(t["offset"] + t["size"])
+    for back in range(2, 200):
+        blob = bytearray(enc[int(t["offset"]):end].tobytes())
+        blob[len(blob) - back] ^= 0xFF
+        if oracle.unpack_parallel(bytes(blob))[0] != 0:
+            enc[end - back] ^= 0xFF
+            return
+    raise AssertionError("no rejected flip found")
+
+
+def test_plan_reports_corrupt_blocks(hip, oracle):
+    """A block whose code bits the oracle rejects is the only one reported, with a
+    stream error, and every other block decodes exactly."""
     w = syn.normal_bf16(41, (64, 4096))
     enc, table = hip.encode_tensor(w, 2)
     enc = enc.copy()
-    t2 = table[2]
-    enc[t2["offset"] + t2["size"] - 3] ^= 0xFF  # flip bits in substream 31's code stream of block 2
+    _corrupt_code_bits(oracle, enc, table[2])
     d_arc = _upload(enc)
     out = torch.zeros(w.nbytes, dtype=torch.uint8, device="cuda")
     plan = xksv_hip.Plan(hip, table, enc.nbytes)
     plan.decode(d_arc.data_ptr(), out.data_ptr(), out.numel())
     n, first, bits = plan.errors()
-    rc, _ = hip.try_unpack_parallel(enc[t2["offset"]:t2["offset"] + t2["size"]].tobytes())
-    assert (n == 0) == (rc == 0)
-    if n:
-        assert first == 2 and bits
+    assert (n, first) == (1, 2) and bits == xksv_hip.ERR_STREAM
     host = out.cpu().numpy()
     for b in (0, 1, 3):
         assert host[b * 131072:(b + 1) * 131072].tobytes() == raw_bytes(w[16 * b:16 * b + 16])
@@ -132,7 +142,7 @@ def test_plan_gemv_whole_tensor(hip, codec, shape):
 
 
 @pytest.mark.parametrize("batch", [1, 8])
-def test_plan_gemm_reports_corrupt_blocks(hip, batch):
+def test_plan_gemm_reports_corrupt_blocks(hip, oracle, batch):
     """Fused GEMM by substream: a block whose XKSP2 header is damaged (block 1)
     and one whose substream code bits are damaged (block 3) are reported, their
     Y rows are left untouched, and every other block's rows are exact."""
@@ -144,8 +154,8 @@ def test_plan_gemm_reports_corrupt_blocks(hip, batch):
     table["out_offset"] //= cols * 2
     t1, t3 = table[1], table[3]
     enc[t1["offset"]] ^= 0x01                       # magic
-    enc[t3["offset"] + t3["size"] - 3] ^= 0xFF      # code bits of the last substream
-    rc3, _ = hip.try_unpack_parallel(enc[t3["offset"]:t3["offset"] + t3["size"]].tobytes())
+    _corrupt_code_bits(oracle, enc, t3)             # code bits of the last substream
+    assert oracle.unpack_parallel(enc[t1["offset"]:t1["offset"] + t1["size"]].tobytes())[0] != 0
     d_arc = _upload(enc)
     plan = xksv_hip.Plan(hip, table, enc.nbytes)
     g = torch.Generator(device="cuda")
@@ -154,11 +164,11 @@ def test_plan_gemm_reports_corrupt_blocks(hip, batch):
     y = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
     plan.gemm_bf16(d_arc.data_ptr(), x.data_ptr(), batch, y.data_ptr())
     n, first, bits = plan.errors()
-    assert first == 1 and bits and n == (1 if rc3 == 0 else 2)
+    assert (n, first) == (2, 1) and bits == xksv_hip.ERR_HEADER | xksv_hip.ERR_STREAM
     got = y.cpu().numpy()
     wt = torch.from_numpy(syn.bf16_to_f32(w).astype(np.float64)).to("cuda")
     want = (x.double() @ wt.T).cpu().numpy()
-    bad = {1} | ({3} if rc3 else set())
+    bad = {1, 3}
     for b in range(rows // 16):
         sl = got[:, 16 * b:16 * b + 16]
         if b in bad:
@@ -167,3 +177,52 @@ def test_plan_gemm_reports_corrupt_blocks(hip, batch):
             err = np.linalg.norm(sl - want[:, 16 * b:16 * b + 16]) / np.linalg.norm(want[:, 16 * b:16 * b + 16])
             assert err <= 1e-5, (b, err)
     plan.close()
+
+
+def _resplit(hip, oracle, w, chunks) -> bytes:
+    """An XKSP2 block of slab `w` (16 rows) with `chunks` substreams (src/c_api.cpp:44-65
+    layout; any chunk count <= 32 is valid, src/c_api.cpp:66-72)."""
+    rows, cols = w.shape
+    tiled = oracle.tile(w, rows, cols)
+    n = rows * cols
+    segs = [hip.call("xksv_pack", raw_bytes(tiled[n * i // chunks:n * (i + 1) // chunks]), 1,
+                     n * (i + 1) // chunks - n * i // chunks) for i in range(chunks)]
+    blob = (b"XKSP2\0\0\0" + rows.to_bytes(8, "little") + cols.to_bytes(8, "little") + chunks.to_bytes(8, "little") +
+            b"".join(len(s).to_bytes(8, "little") for s in segs) + b"".join(segs))
+    assert oracle.unpack_parallel(blob) == (0, raw_bytes(w))
+    return blob
+
+
+@pytest.mark.parametrize("batch", [1, 3, 8])
+def test_plan_gemm_nonstandard_chunk_counts(hip, oracle, batch):
+    """Plan GEMMs over XKSP2 blocks re-split into 32, 5, 7, 1, 31 and 16 substreams: blocks
+    whose substreams do not start on 8-element boundaries are routed to decode + plain GEMM,
+    the others to the fused kernels; fp32 X and bf16 X (MFMA from batch 8) both match fp64."""
+    cols = 1024
+    counts = (32, 5, 7, 1, 31, 16)
+    w = syn.normal_bf16(900 + batch, (16 * len(counts), cols))
+    blobs = [_resplit(hip, oracle, w[16 * i:16 * i + 16], c) for i, c in enumerate(counts)]
+    enc = np.frombuffer(b"".join(blobs), np.uint8)
+    table = np.zeros(len(blobs), xksv_hip.BLOCK_DTYPE)
+    off = 0
+    for i, b in enumerate(blobs):
+        table[i] = (off, len(b), 16 * cols * 2, 16 * i, 16, cols, xksv_hip.CODEC_PARALLEL, 0)
+        off += len(b)
+    d_arc = _upload(enc)
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    wt = torch.from_numpy(syn.bf16_to_f32(w).astype(np.float64)).to("cuda")
+    try:
+        x = torch.randn(cols, batch, dtype=torch.float32, device="cuda")
+        y = torch.full((16 * len(counts), batch), float("nan"), dtype=torch.float32, device="cuda")
+        plan.gemm(d_arc.data_ptr(), x.data_ptr(), batch, y.data_ptr())
+        assert plan.errors()[0] == 0
+        want = (wt @ x.double()).cpu().numpy()
+        assert np.linalg.norm(y.cpu().numpy() - want) / np.linalg.norm(want) <= 1e-5
+        xb = torch.randn(batch, cols, device="cuda").to(torch.bfloat16).contiguous()
+        yb = torch.full((batch, 16 * len(counts)), float("nan"), dtype=torch.float32, device="cuda")
+        plan.gemm_bf16(d_arc.data_ptr(), xb.data_ptr(), batch, yb.data_ptr())
+        assert plan.errors()[0] == 0
+        want = (xb.double() @ wt.T).cpu().numpy()
+        assert np.linalg.norm(yb.cpu().numpy() - want) / np.linalg.norm(want) <= 2e-3
+    finally:
+        plan.close()

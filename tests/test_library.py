@@ -119,3 +119,17 @@ def test_encode_tensor_worker_count_determinism(hip, codec):
     for threads in (2, 3, 8):
         enc, table = hip.encode_tensor(w, codec, threads=threads)
         assert enc.tobytes() == ref_enc.tobytes() and table.tobytes() == ref_table.tobytes()
+
+
+def test_encode_tensor_rejects_odd_bf16_byte_count(hip):
+    """An odd byte count cannot be BF16 words: the encoder refuses it (a 1-byte tail
+    would fit no slab) instead of looping."""
+    import ctypes
+    data = np.zeros(4097, np.uint8)
+    out, size = ctypes.c_void_p(), ctypes.c_uint64()
+    blocks, nblocks = ctypes.POINTER(xksv_hip.Block)(), ctypes.c_uint64()
+    rc = hip.lib.xksv_encode_tensor(data.ctypes.data, data.nbytes, 1, 0, 2, 1, ctypes.byref(out),
+                                    ctypes.byref(size), ctypes.byref(blocks), ctypes.byref(nblocks))
+    assert rc == -1
+    enc, table = hip.encode_tensor(data.view(np.uint8), 2, bf16=False)
+    assert len(table) == 1 and table["codec"][0] == xksv_hip.CODEC_RAW and enc.tobytes() == data.tobytes()

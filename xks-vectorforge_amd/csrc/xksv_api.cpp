@@ -292,10 +292,15 @@ bool upload(const std::vector<DevBlock>& v, DevBlock** dst) {
   return hipMemcpy(*dst, v.data(), v.size() * sizeof(DevBlock), hipMemcpyHostToDevice) == hipSuccess;
 }
 
-// GEMM routing: fused kernels for 16-row compressed slabs of whole tiles,
-// decode-to-scratch + plain GEMM for other compressed slabs, plain GEMM
-// straight from the archive for raw slabs.
-bool prepare_gemm(xksv_hip_plan* P) {
+// GEMM routing: fused kernels for 16-row compressed slabs whose streams start
+// and end on 8-element boundaries, decode-to-scratch + plain GEMM for other
+// compressed slabs, plain GEMM straight from the archive for raw slabs.  For
+// XKSP2 slabs the substream boundaries depend on the block's chunk count, so
+// a header pre-pass over the archive of the first GEMM call routes them (one
+// synchronisation); later calls take archives with the same block headers
+// (copies of one archive), and a block whose header no longer fits the fused
+// kernels is reported by them as a shape error.
+bool prepare_gemm(xksv_hip_plan* P, const uint8_t* arc, hipStream_t s) {
   if (P->gemm_ready) return P->gemm_valid;
   P->gemm_ready = true;
   uint64_t cols = 0;
@@ -305,8 +310,31 @@ bool prepare_gemm(xksv_hip_plan* P) {
     for (const auto& b : P->blocks)
       if (b.cols) cols = b.cols;
   if (!cols) return false;
+  // XKSP2 candidates for the fused kernels: their header decides.
+  std::vector<DevBlock> cand;
+  for (size_t i = 0; i < P->blocks.size(); ++i) {
+    const auto& b = P->blocks[i];
+    if (b.codec == XKSV_CODEC_PARALLEL && b.cols == cols && b.rows == 16 && cols % 16 == 0)
+      cand.push_back(DevBlock{b.offset, b.size, b.out_offset, b.rows, cols, b.codec, (uint32_t)i});
+  }
+  std::vector<uint32_t> route(P->blocks.size(), 3u);
+  if (!cand.empty()) {
+    DevBlock* d_cand = nullptr;
+    uint32_t* d_flags = nullptr;
+    std::vector<uint32_t> flags(cand.size());
+    bool ok = upload(cand, &d_cand) &&
+              hipMalloc(reinterpret_cast<void**>(&d_flags), cand.size() * 4) == hipSuccess &&
+              launch_route_parallel(d_cand, (uint32_t)cand.size(), arc, d_flags, s) == hipSuccess &&
+              hipStreamSynchronize(s) == hipSuccess &&
+              hipMemcpy(flags.data(), d_flags, cand.size() * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    if (d_cand) (void)hipFree(d_cand);
+    if (d_flags) (void)hipFree(d_flags);
+    if (!ok) return false;
+    for (size_t j = 0; j < cand.size(); ++j) route[cand[j].status_slot] = flags[j];
+  }
   std::vector<DevBlock> fs, fp, gds, gdp, gp, raw;
   uint64_t scratch = 0, rows_extent = 0;
+  bool tile = true;
   for (size_t i = 0; i < P->blocks.size(); ++i) {
     const auto& b = P->blocks[i];
     const uint32_t slot = (uint32_t)i;
@@ -317,11 +345,12 @@ bool prepare_gemm(xksv_hip_plan* P) {
       raw.push_back(DevBlock{b.offset, b.size, b.out_offset, rows, cols, kCodecRaw, slot});
     } else {
       if (b.cols != cols) return false;
-      const bool fused = b.rows == 16 && cols % 16 == 0;
-      if (fused)
+      const bool fused = b.rows == 16 && cols % 16 == 0 && (route[i] & 1u);
+      if (fused) {
+        if (b.codec == XKSV_CODEC_PARALLEL) tile = tile && (route[i] & 2u);
         (b.codec == XKSV_CODEC_SERIAL ? fs : fp).push_back(DevBlock{b.offset, b.size, b.out_offset, b.rows, cols,
                                                                     b.codec, slot});
-      else {
+      } else {
         (b.codec == XKSV_CODEC_SERIAL ? gds : gdp).push_back(DevBlock{b.offset, b.size, scratch, b.rows, cols, b.codec, slot});
         gp.push_back(DevBlock{scratch, 0, b.out_offset, b.rows, cols, kCodecRaw, slot});
         scratch += align_up(b.raw_size, 16);
@@ -340,9 +369,8 @@ bool prepare_gemm(xksv_hip_plan* P) {
   P->n_gpar = (uint32_t)gdp.size();
   P->n_generic = (uint32_t)gp.size();
   P->n_graw = (uint32_t)raw.size();
-  // The reference's encoder splits a 16-row slab into 32 substreams of 16 *
-  // cols / 32 elements: whole tiles when cols is a multiple of 512.
-  P->tile_parallel = cols % 512 == 0;
+  // The MFMA consumer needs every fused XKSP2 substream to cover whole tiles.
+  P->tile_parallel = tile;
   if (scratch && hipMalloc(reinterpret_cast<void**>(&P->scratch), scratch) != hipSuccess) return false;
   // Substream partial sums for the fused XKSP2 list: 32 KiB per block, up to
   // kMaxItemMem; larger lists keep the workgroup-per-block kernels.
@@ -543,9 +571,9 @@ static int plan_gemm(xksv_hip_plan* P, const void* archive, const void* x, size_
                      bool bf16) {
   if (!P || !archive || !x || !y || !batch) return 1;
   const DeviceInfo* di = current_device(nullptr);
-  if (!di || !prepare_gemm(P)) return 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* arc = static_cast<const uint8_t*>(archive);
+  if (!di || !prepare_gemm(P, arc, s)) return 1;
   const unsigned cus = (unsigned)di->cus;
   uint32_t* queue = P->status + P->blocks.size();
   const float* xf = static_cast<const float*>(x);

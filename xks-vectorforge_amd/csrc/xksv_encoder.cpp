@@ -298,7 +298,10 @@ int xksv_pack_parallel(const void* data, size_t n, size_t rows, size_t cols, voi
 int xksv_encode_tensor(const void* data, uint64_t nbytes, int bf16, uint64_t shape_cols, uint32_t codec,
                        uint32_t threads, void** out, uint64_t* out_size, xksv_hip_block** blocks,
                        uint64_t* nblocks) {
-  if (!out || !out_size || !blocks || !nblocks || (nbytes && !data) || (codec != 1 && codec != 2)) return -1;
+  // BF16 data is whole 2-byte words (an odd count would leave a 1-byte tail no slab can hold).
+  if (!out || !out_size || !blocks || !nblocks || (nbytes && !data) || (codec != 1 && codec != 2) ||
+      (bf16 && nbytes % 2))
+    return -1;
   try {
     const std::vector<SlabSpec> slabs = slab_rule(nbytes, bf16 != 0, shape_cols);
     std::vector<std::vector<uint8_t>> enc(slabs.size());

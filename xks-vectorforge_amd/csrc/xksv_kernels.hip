@@ -1744,6 +1744,34 @@ __global__ void __launch_bounds__(64) k_gemm_plain_bf16(const DevBlock* __restri
   }
 }
 
+// Routing of XKSP2 blocks for the fused GEMM, from each block's header:
+// bit 0 = every substream starts and ends on an 8-element boundary (the fused
+// VALU consumers apply), bit 1 = on 256-element boundaries (whole 16x16 tiles:
+// the MFMA consumer applies).  A header that does not parse, or disagrees with
+// the descriptor, gets both bits: the fused kernels then report its error.
+__global__ void __launch_bounds__(256) k_route_parallel(const DevBlock* __restrict__ blocks, uint32_t n,
+                                                        const uint8_t* __restrict__ arc, uint32_t* __restrict__ flags) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const DevBlock d = blocks[i];
+    uint32_t f = 3;
+    if (d.size >= 32) {
+      const uint8_t* p = arc + d.src;
+      const uint64_t magic = ldg64(p), rows = ldg64(p + 8), cols = ldg64(p + 16), chunks = ldg64(p + 24);
+      if (magic == kMagicXKSP2 && rows == d.rows && cols == d.cols && rows && rows <= 16 && cols &&
+          cols <= kMaxBlockElems / rows && chunks && chunks <= kMaxChunks && chunks <= rows * cols) {
+        const uint64_t total = rows * cols;
+        for (uint64_t k = 1; k <= chunks; ++k) {
+          const uint64_t b = total * k / chunks;
+          if (b % 8) f &= ~1u;
+          if (b % 256) f &= ~2u;
+        }
+        if (!(f & 1u)) f = 0;
+      }
+    }
+    flags[i] = f;
+  }
+}
+
 __global__ void k_fill_u32(uint32_t* p, uint64_t n, uint32_t v) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
     p[i] = v;
@@ -1861,6 +1889,14 @@ hipError_t launch_gemm_plain_bf16(const DevBlock* blocks, uint32_t nblocks, cons
   if (!nblocks) return hipSuccess;
   hipLaunchKernelGGL(k_gemm_plain_bf16, dim3(256, nblocks < 256 ? nblocks : 256), dim3(64), 0, s, blocks, nblocks,
                      base, x, ldx, nb, y, ldy);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_parallel(const DevBlock* blocks, uint32_t n, const uint8_t* arc, uint32_t* flags,
+                                 hipStream_t s) {
+  if (!n) return hipSuccess;
+  const unsigned g = (n + 255) / 256;
+  hipLaunchKernelGGL(k_route_parallel, dim3(g < 1024 ? g : 1024u), dim3(256), 0, s, blocks, n, arc, flags);
   return hipGetLastError();
 }
 
