@@ -87,6 +87,19 @@ int xksv_hip_gemm_parallel(const void* input, size_t n, size_t batch, const floa
  * below that on fp32 VALU FMAs. */
 int xksv_hip_gemm_parallel_bf16(const void* input, size_t n, size_t batch, const uint16_t* x, float* output);
 
+/* No reference counterpart.  For callers that cannot allocate device memory
+ * (serving loops, harnesses that forbid hipMalloc): xksv_hip_gemm_parallel
+ * with the same arguments, kernels and results, staged in a fixed device array
+ * of XKSV_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends) instead
+ * of allocated buffers; it calls no hipMalloc/hipFree.  Returns 0 on success,
+ * 1 on any validation, bitstream or HIP error, 2 when the call's staging (the
+ * encoded block plus its 32 KiB of substream partial sums, or plus its decoded
+ * slab when the substreams are not unit-aligned) exceeds the array; every
+ * block the archive compiler writes (at most 1 MiB raw) fits.  Calls on one
+ * GPU share the array: they take turns under a per-device host lock. */
+#define XKSV_NOALLOC_SCRATCH_BYTES ((4u << 20) + (64u << 10))
+int xksv_hip_gemm_parallel_noalloc(const void* input, size_t n, size_t batch, const float* x, float* output);
+
 /* Reference names, same functions. */
 int xksv_cuda_decode(const void* input, size_t size, size_t rows, size_t cols, void* output);
 int xksv_cuda_gemv(const void* input, size_t size, size_t rows, size_t cols, const float* x, float* output);

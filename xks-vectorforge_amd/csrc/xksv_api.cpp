@@ -96,121 +96,20 @@ void release(int dev, Buf b) {
   g_pool[dev].push_back(b);
 }
 
-// Staging layout for one block: [2 descriptors][status][block][scratch].
-struct Layout {
-  uint64_t desc = 0, status, block, scratch, total;
-  Layout(uint64_t block_size, uint64_t scratch_size) {
-    status = align_up(desc + 2 * sizeof(DevBlock), kAlign);
-    block = status + kAlign;
-    scratch = align_up(block + block_size + 16, kAlign);
-    total = scratch + align_up(scratch_size, kAlign);
-  }
-};
-
-// What a block-level call computes.  kDecode: BF16 into `out` (device).
-// kGemmF32: fused GEMM with fp32 X [cols, batch] into Y [rows, batch].
-// kGemmBf16: fused GEMM with bf16 X [batch, cols] into fp32 Y [batch, rows]
-// (bf16 MFMA from batch 8 when every substream covers whole tiles).
-enum Mode { kDecode, kGemmF32, kGemmBf16 };
-struct Fused {
-  bool unit = false;  // every stream unit-aligned: fused consumers apply
-  bool tile = false;  // every stream covers whole 16x16 tiles: MFMA applies
-};
-
-// One block through the GPU.
+// One block through the GPU, staged in a pooled device buffer.
 int run_block(const uint8_t* input, uint64_t size, uint32_t codec, uint64_t rows, uint64_t cols, Fused fused,
               Mode mode, void* out, const void* x, uint64_t batch) {
   int dev = -1;
   const DeviceInfo* di = current_device(&dev);
   if (!di) return 1;
-  const uint64_t n = rows * cols;
-  const bool generic_gemm = mode != kDecode && !fused.unit;
-  // Fused GEMM over an XKSP2 block runs by substream (item scratch).
-  const bool items = mode != kDecode && !generic_gemm && codec == kCodecParallel;
-  Layout L(size, generic_gemm ? n * 2 : items ? kItemScratchPerBlock : 0);
+  const BlockLayout L = block_layout(size, codec, rows, cols, fused, mode);
   Buf b;
   if (!acquire(dev, L.total, b)) return 1;
-  int rc = 1;
-  do {
-    DevBlock d[2];
-    d[0] = DevBlock{L.block, size, 0, rows, cols, codec, 0};
-    d[1] = DevBlock{L.scratch, 0, 0, rows, cols, kCodecRaw, 0};
-    if (hipMemcpy(b.p + L.desc, d, sizeof d, hipMemcpyHostToDevice) != hipSuccess) break;
-    if (hipMemcpy(b.p + L.block, input, size, hipMemcpyHostToDevice) != hipSuccess) break;
-    uint32_t* status = reinterpret_cast<uint32_t*>(b.p + L.status);
-    if (launch_fill_u32(status, kAlign / 4, 0, nullptr) != hipSuccess) break;
-    const DevBlock* dd = reinterpret_cast<const DevBlock*>(b.p + L.desc);
-    const unsigned cus = (unsigned)di->cus;
-    const ItemScratch is{reinterpret_cast<float*>(b.p + L.scratch),
-                         reinterpret_cast<uint32_t*>(b.p + L.scratch + kItemScratchPerBlock - 4)};
-    float* y = static_cast<float*>(out);
-    if (mode == kDecode) {
-      if (launch_decode(dd, 1, codec, b.p, static_cast<uint8_t*>(out), status, nullptr, cus, nullptr) != hipSuccess)
-        break;
-    } else if (!generic_gemm) {
-      bool ok = true;
-      for (uint64_t j0 = 0; j0 < batch && ok; j0 += kMaxFusedBatch) {
-        const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
-        if (mode == kGemmF32)
-          ok = launch_gemm_f32(dd, 1, codec, b.p, static_cast<const float*>(x) + j0, batch, nb, y + j0, batch, status,
-                               items ? &is : nullptr, cus, nullptr) == hipSuccess;
-        else
-          ok = launch_gemm_bf16(dd, 1, codec, b.p, static_cast<const uint16_t*>(x) + j0 * cols, cols, nb,
-                                y + j0 * rows, rows, fused.tile, status, items ? &is : nullptr, cus,
-                                nullptr) == hipSuccess;
-      }
-      if (!ok) break;
-    } else {
-      // Not unit-aligned: decode to scratch, then a plain deterministic GEMM.
-      if (launch_decode(dd, 1, codec, b.p, b.p + L.scratch, status, nullptr, cus, nullptr) != hipSuccess) break;
-      const hipError_t e =
-          mode == kGemmF32
-              ? launch_gemm_plain(dd + 1, 1, b.p, static_cast<const float*>(x), batch, (uint32_t)batch, y, batch,
-                                  nullptr)
-              : launch_gemm_plain_bf16(dd + 1, 1, b.p, static_cast<const uint16_t*>(x), cols, (uint32_t)batch, y,
-                                       rows, nullptr);
-      if (e != hipSuccess) break;
-    }
-    if (hipStreamSynchronize(nullptr) != hipSuccess) break;
-    uint32_t st = 1;
-    if (hipMemcpy(&st, status, 4, hipMemcpyDeviceToHost) != hipSuccess) break;
-    rc = st ? 1 : 0;
-  } while (0);
+  const int rc = run_block_at(b.p, L, input, size, codec, rows, cols, fused, mode, out, x, batch, (unsigned)di->cus);
   release(dev, b);
   return rc;
 }
 
-struct ParallelHeader {
-  uint64_t rows, cols, chunks;
-};
-// Shape fields of an XKSP2 block, with the reference's header checks
-// (cuda/parallel.cu:132-134); the kernel repeats them and validates the rest.
-bool parallel_header(const uint8_t* p, uint64_t n, ParallelHeader& h) {
-  if (!p || n < 32 || memcmp(p, "XKSP2\0\0\0", 8)) return false;
-  h.rows = get64(p + 8);
-  h.cols = get64(p + 16);
-  h.chunks = get64(p + 24);
-  if (!h.rows || h.rows > 16 || !h.cols || !h.chunks || h.chunks > 32 || h.cols > UINT64_MAX / h.rows ||
-      h.chunks > h.rows * h.cols || h.rows * h.cols > n || h.rows * h.cols > UINT64_MAX / 32 || n < 32 + 8 * h.chunks)
-    return false;
-  return h.rows * h.cols <= kMaxBlockElems;
-}
-
-// Fused kernels need 16-row slabs of whole tiles whose streams start and end
-// on 8-element boundaries; the MFMA consumer needs them on tile boundaries.
-Fused fused_parallel(const ParallelHeader& h) {
-  Fused f;
-  if (h.rows != 16 || h.cols % 16) return f;
-  const uint64_t total = h.rows * h.cols;
-  f.unit = f.tile = true;
-  for (uint64_t k = 0; k <= h.chunks; ++k) {
-    const uint64_t b = total * k / h.chunks;
-    f.unit = f.unit && b % 8 == 0;
-    f.tile = f.tile && b % 256 == 0;
-  }
-  f.tile = f.tile && f.unit;
-  return f;
-}
 Fused fused_serial(uint64_t rows, uint64_t cols) {
   Fused f;
   f.unit = f.tile = rows == 16 && cols % 16 == 0;
@@ -258,6 +157,101 @@ int unpack_via_gpu(const uint8_t* p, uint64_t n, uint32_t codec, uint64_t rows, 
 }  // namespace
 
 // ------------------------------------------------------------ plan object
+
+namespace xksv {
+
+// Shape fields of an XKSP2 block, with the reference's header checks
+// (cuda/parallel.cu:132-134); the kernel repeats them and validates the rest.
+bool parallel_header(const uint8_t* p, uint64_t n, ParallelHeader& h) {
+  if (!p || n < 32 || memcmp(p, "XKSP2\0\0\0", 8)) return false;
+  h.rows = get64(p + 8);
+  h.cols = get64(p + 16);
+  h.chunks = get64(p + 24);
+  if (!h.rows || h.rows > 16 || !h.cols || !h.chunks || h.chunks > 32 || h.cols > UINT64_MAX / h.rows ||
+      h.chunks > h.rows * h.cols || h.rows * h.cols > n || h.rows * h.cols > UINT64_MAX / 32 || n < 32 + 8 * h.chunks)
+    return false;
+  return h.rows * h.cols <= kMaxBlockElems;
+}
+
+// Fused kernels need 16-row slabs of whole tiles whose streams start and end
+// on 8-element boundaries; the MFMA consumer needs them on tile boundaries.
+Fused fused_parallel(const ParallelHeader& h) {
+  Fused f;
+  if (h.rows != 16 || h.cols % 16) return f;
+  const uint64_t total = h.rows * h.cols;
+  f.unit = f.tile = true;
+  for (uint64_t k = 0; k <= h.chunks; ++k) {
+    const uint64_t b = total * k / h.chunks;
+    f.unit = f.unit && b % 8 == 0;
+    f.tile = f.tile && b % 256 == 0;
+  }
+  f.tile = f.tile && f.unit;
+  return f;
+}
+BlockLayout block_layout(uint64_t size, uint32_t codec, uint64_t rows, uint64_t cols, Fused fused, Mode mode) {
+  const uint64_t n = rows * cols;
+  const bool generic_gemm = mode != kDecode && !fused.unit;
+  const bool items = mode != kDecode && !generic_gemm && codec == kCodecParallel;
+  const uint64_t scratch_size = generic_gemm ? n * 2 : items ? kItemScratchPerBlock : 0;
+  BlockLayout L;
+  L.desc = 0;
+  L.status = align_up(L.desc + 2 * sizeof(DevBlock), kAlign);
+  L.block = L.status + kAlign;
+  L.scratch = align_up(L.block + size + 16, kAlign);
+  L.total = L.scratch + align_up(scratch_size, kAlign);
+  return L;
+}
+
+int run_block_at(uint8_t* base, const BlockLayout& L, const uint8_t* input, uint64_t size, uint32_t codec,
+                 uint64_t rows, uint64_t cols, Fused fused, Mode mode, void* out, const void* x, uint64_t batch,
+                 unsigned cus) {
+  const bool generic_gemm = mode != kDecode && !fused.unit;
+  // Fused GEMM over an XKSP2 block runs by substream (item scratch).
+  const bool items = mode != kDecode && !generic_gemm && codec == kCodecParallel;
+  DevBlock d[2];
+  d[0] = DevBlock{L.block, size, 0, rows, cols, codec, 0};
+  d[1] = DevBlock{L.scratch, 0, 0, rows, cols, kCodecRaw, 0};
+  if (hipMemcpy(base + L.desc, d, sizeof d, hipMemcpyHostToDevice) != hipSuccess) return 1;
+  if (hipMemcpy(base + L.block, input, size, hipMemcpyHostToDevice) != hipSuccess) return 1;
+  uint32_t* status = reinterpret_cast<uint32_t*>(base + L.status);
+  if (launch_fill_u32(status, kAlign / 4, 0, nullptr) != hipSuccess) return 1;
+  const DevBlock* dd = reinterpret_cast<const DevBlock*>(base + L.desc);
+  const ItemScratch is{reinterpret_cast<float*>(base + L.scratch),
+                       reinterpret_cast<uint32_t*>(base + L.scratch + kItemScratchPerBlock - 4)};
+  float* y = static_cast<float*>(out);
+  if (mode == kDecode) {
+    if (launch_decode(dd, 1, codec, base, static_cast<uint8_t*>(out), status, nullptr, cus, nullptr) != hipSuccess)
+      return 1;
+  } else if (!generic_gemm) {
+    for (uint64_t j0 = 0; j0 < batch; j0 += kMaxFusedBatch) {
+      const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
+      const hipError_t e =
+          mode == kGemmF32
+              ? launch_gemm_f32(dd, 1, codec, base, static_cast<const float*>(x) + j0, batch, nb, y + j0, batch,
+                                status, items ? &is : nullptr, cus, nullptr)
+              : launch_gemm_bf16(dd, 1, codec, base, static_cast<const uint16_t*>(x) + j0 * cols, cols, nb,
+                                 y + j0 * rows, rows, fused.tile, status, items ? &is : nullptr, cus, nullptr);
+      if (e != hipSuccess) return 1;
+    }
+  } else {
+    // Not unit-aligned: decode to scratch, then a plain deterministic GEMM.
+    if (launch_decode(dd, 1, codec, base, base + L.scratch, status, nullptr, cus, nullptr) != hipSuccess) return 1;
+    const hipError_t e =
+        mode == kGemmF32
+            ? launch_gemm_plain(dd + 1, 1, base, static_cast<const float*>(x), batch, (uint32_t)batch, y, batch,
+                                nullptr)
+            : launch_gemm_plain_bf16(dd + 1, 1, base, static_cast<const uint16_t*>(x), cols, (uint32_t)batch, y,
+                                     rows, nullptr);
+    if (e != hipSuccess) return 1;
+  }
+  if (hipStreamSynchronize(nullptr) != hipSuccess) return 1;
+  uint32_t st = 1;
+  if (hipMemcpy(&st, status, 4, hipMemcpyDeviceToHost) != hipSuccess) return 1;
+  return st ? 1 : 0;
+}
+
+}  // namespace xksv
+
 
 struct xksv_hip_plan {
   int device = -1;

@@ -18,6 +18,37 @@ bool encode_serial(const uint8_t* data, uint64_t rows, uint64_t cols, std::vecto
 bool encode_parallel(const uint8_t* data, uint64_t rows, uint64_t cols, std::vector<uint8_t>& v);
 std::vector<SlabSpec> slab_rule(uint64_t nbytes, bool bf16, uint64_t shape_cols);
 
+// What a block-level call computes.  kDecode: BF16 into `out` (device).
+// kGemmF32: fused GEMM with fp32 X [cols, batch] into Y [rows, batch].
+// kGemmBf16: fused GEMM with bf16 X [batch, cols] into fp32 Y [batch, rows]
+// (bf16 MFMA from batch 8 when every substream covers whole tiles).
+enum Mode { kDecode, kGemmF32, kGemmBf16 };
+struct Fused {
+  bool unit = false;  // every stream unit-aligned: fused consumers apply
+  bool tile = false;  // every stream covers whole 16x16 tiles: MFMA applies
+};
+// Shape fields of an XKSP2 block with the reference's header checks
+// (cuda/parallel.cu:132-134); false when they fail.
+struct ParallelHeader {
+  uint64_t rows, cols, chunks;
+};
+bool parallel_header(const uint8_t* p, uint64_t n, ParallelHeader& h);
+// Which fused consumers apply to an XKSP2 block of this header.
+Fused fused_parallel(const ParallelHeader& h);
+// Device staging of one block-level call, byte offsets from its base:
+// [2 descriptors][status words][encoded block][scratch: item partial sums of
+// a fused XKSP2 GEMM, or the decoded slab of a GEMM that is not unit-aligned].
+struct BlockLayout {
+  uint64_t desc, status, block, scratch, total;
+};
+BlockLayout block_layout(uint64_t size, uint32_t codec, uint64_t rows, uint64_t cols, Fused fused, Mode mode);
+// One block-level call staged at device memory `base` (layout L): copies the
+// host block in, launches on the null stream, synchronises, reads the status.
+// 0 on success, 1 on any validation, bitstream or HIP error.
+int run_block_at(uint8_t* base, const BlockLayout& L, const uint8_t* input, uint64_t size, uint32_t codec,
+                 uint64_t rows, uint64_t cols, Fused fused, Mode mode, void* out, const void* x, uint64_t batch,
+                 unsigned cus);
+
 // Kernel launchers (xksv_kernels.hip).  `cus` = the device's CU count; each
 // launcher sizes its persistent grid to the workgroups resident at once.
 // `queue` (optional) is a zeroed counter the decode waves claim blocks from.

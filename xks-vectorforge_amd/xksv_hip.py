@@ -53,6 +53,7 @@ _SIGNATURES = {
     "xksv_hip_gemv_parallel": (_int, [_vp, _sz, _vp, _vp]),
     "xksv_hip_gemm_parallel": (_int, [_vp, _sz, _sz, _vp, _vp]),
     "xksv_hip_gemm_parallel_bf16": (_int, [_vp, _sz, _sz, _vp, _vp]),
+    "xksv_hip_gemm_parallel_noalloc": (_int, [_vp, _sz, _sz, _vp, _vp]),
     "xksv_cuda_decode": (_int, [_vp, _sz, _sz, _sz, _vp]),
     "xksv_cuda_gemv": (_int, [_vp, _sz, _sz, _sz, _vp, _vp]),
     "xksv_cuda_gemm": (_int, [_vp, _sz, _sz, _sz, _sz, _vp, _vp]),
@@ -150,6 +151,11 @@ class Library:
     def gemm_parallel(self, block: bytes, batch: int, x_ptr: int, y_ptr: int) -> int:
         return self.lib.xksv_hip_gemm_parallel(ctypes.create_string_buffer(bytes(block), max(len(block), 1)),
                                                len(block), batch, x_ptr, y_ptr)
+
+    def gemm_parallel_noalloc(self, block: bytes, batch: int, x_ptr: int, y_ptr: int) -> int:
+        """xksv_hip_gemm_parallel staged in the library's fixed device array (no allocation)."""
+        return self.lib.xksv_hip_gemm_parallel_noalloc(ctypes.create_string_buffer(bytes(block), max(len(block), 1)),
+                                                       len(block), batch, x_ptr, y_ptr)
 
     def gemm_parallel_bf16(self, block: bytes, batch: int, x_ptr: int, y_ptr: int) -> int:
         """bf16 X [batch, cols] -> fp32 Y [batch, rows] (layout of x @ W.T)."""
