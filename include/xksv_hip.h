@@ -10,7 +10,9 @@
  * the reference's; the block format (.xksv serial "bf16-huffman-tile16" and
  * XKSP2 "bf16-huffman-parallel32" blocks) is unchanged.  Plain pointers and
  * sizes only.  Decoding always runs on the GPU: without a HIP device every
- * decode entry point fails (returns its error value).
+ * decode entry point fails (returns its error value), xksv_unpack and
+ * xksv_unpack_parallel included -- there is no CPU decode in this library, so
+ * CPU-only consumers of the codec keep the reference's libxksv_native.so.
  */
 #ifndef XKSV_HIP_H
 #define XKSV_HIP_H

@@ -6,6 +6,7 @@ from __future__ import annotations
 
 import ctypes
 import hashlib
+import os
 import sys
 from pathlib import Path
 
@@ -15,7 +16,7 @@ ROOT = Path(__file__).resolve().parents[1]
 sys.path.insert(0, str(ROOT / "xks-vectorforge_amd"))
 import xksv_synth as syn  # noqa: E402
 
-ORACLE_SO = ROOT / "oracle" / "liboracle.so"
+ORACLE_SO = Path(os.environ.get("XKSV_ORACLE_LIBRARY", ROOT / "oracle" / "liboracle.so"))
 REF_SO = ROOT / "oracle" / "_ref" / "libxksv_ref.so"
 
 
