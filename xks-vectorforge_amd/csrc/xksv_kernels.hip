@@ -545,15 +545,27 @@ __device__ __forceinline__ void slide(const Smem& S, uint32_t p, uint32_t& wb, u
 }
 
 // Up to two codewords at bit p (lut2 entry layout).  A window without a code
-// of at most 10 bits moves p by kLongLen (past the caller's end); the caller
-// resolves it (resolve_long).  The second codeword may start at or past the
-// caller's end; the caller undoes that after its last step (end_pair).
-// Bit positions stay below kSegBits + kLongLen + 32, inside the staged
-// segment buffer.
+// of at most 10 bits is resolved on the spot with the per-length limits
+// (long_code): the entry becomes that one code.  That branch is rare (codes
+// longer than the table are well under 0.1% of symbols) and, unlike leaving
+// the code to a later round, keeps the other lanes of the wave stepping.  A
+// window that matches no code sets `dead` and returns kDeadMark, whose
+// "consumed" 127 moves p past the caller's end (chunks are at most kChunk
+// bits and paths start at most kSync bits before them).  The second codeword
+// may start at or past the caller's end; the caller undoes that after its
+// last step (end_pair).  Bit positions stay below kSegBits + kLongLen + 32,
+// inside the staged segment buffer.
+constexpr uint32_t kDeadMark = kLongLen << 8;
+static_assert(kChunk + kSync <= kLongLen, "a dead path must leave every chunk");
 __device__ __forceinline__ uint32_t step2(const Smem& S, uint32_t& p, uint32_t& wi, uint32_t& w0, uint32_t& w1,
-                                          uint32_t& w2) {
+                                          uint32_t& w2, uint32_t maxlen, uint32_t& dead) {
   const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
-  const uint32_t e = S.t.f.lut2[win >> (32 - kLutBits)];
+  uint32_t e = S.t.f.lut2[win >> (32 - kLutBits)];
+  if (e == kLongMark) {
+    const uint32_t lc = long_code(S, win, maxlen);  // (len << 8) | symbol: no second symbol, len1 0
+    dead |= lc == 0;
+    e = lc ? lc : kDeadMark;
+  }
   p += (e >> 8) & 127u;
   slide(S, p, wi, w0, w1, w2);
   return e;
@@ -580,48 +592,20 @@ __device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t&
   w2 = S.stream[j + 2];
 }
 
-// The last step's entry `le` was kLongMark: move p back to that step's start
-// and decode the code there with the per-length limits.  A window that
-// matches no code sets `dead` and moves p to `end`.  Returns the code as
-// (len << 8) | symbol, or 0 when dead; `le` becomes a one-symbol entry.
-__device__ __forceinline__ uint32_t resolve_long(const Smem& S, uint32_t& p, uint32_t end, uint32_t& le,
-                                                 uint32_t maxlen, uint32_t& dead, uint32_t& wi, uint32_t& w0,
-                                                 uint32_t& w1, uint32_t& w2) {
-  p -= kLongLen;
-  load_window(S, p, wi, w0, w1, w2);
-  const uint32_t lc = long_code(S, __builtin_amdgcn_alignbit(w0, w1, 0u - p), maxlen);
-  if (lc) {
-    p += lc >> 8;
-    le = lc;  // bits 8-14 = length, no second symbol
-  } else {
-    dead = 1;
-    p = end;
-    le = 0;
-  }
-  load_window(S, p, wi, w0, w1, w2);
-  return lc;
-}
-
 // Decode the codewords that start in [cs, ce) into region[0 ...], two per
 // lookup where the table allows.  When `from` < cs the codewords before cs
 // are decoded and dropped: Huffman codes resynchronise within a few
 // codewords, so a path started kSync bits early almost always meets the true
 // codeword boundaries before cs (the caller verifies it against the previous
 // lane's exit).  Symbols are stored a byte at a time (aligned LDS stores).
-// Codes longer than the table end a lane's inner loop (kLongMark); they are
-// decoded between rounds of it, which every lane takes part in.
+// A path that meets a window matching no code is dead: it produces no start
+// (f = kNoStart) when that happens before cs, and its symbols are never used.
 __device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint32_t cs, uint32_t ce, uint8_t* region,
                                              uint32_t maxlen, Path& P) {
   uint32_t p = from, d = 0, wi, w0, w1, w2, le = 0;
   load_window(S, p, wi, w0, w1, w2);
-  const bool sync = p < cs;
-  for (;;) {  // every lane takes part in the votes
-    while (p < cs) le = step2(S, p, wi, w0, w1, w2);
-    const bool lng = le == kLongMark;
-    if (!__ballot(lng)) break;
-    if (lng) resolve_long(S, p, cs, le, maxlen, d, wi, w0, w1, w2);
-  }
-  if (sync) {
+  if (p < cs) {
+    while (p < cs) le = step2(S, p, wi, w0, w1, w2, maxlen, d);
     end_pair(le, cs, p);
     load_window(S, p, wi, w0, w1, w2);
   }
@@ -630,19 +614,11 @@ __device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint3
   lds_bytes const out = as_lds(region);
   lds_bytes o = out;  // next symbol slot
   le = 0;
-  for (;;) {
-    while (p < ce) {
-      le = step2(S, p, wi, w0, w1, w2);
-      o[0] = (uint8_t)le;
-      o[1] = (uint8_t)(le >> 16);
-      o += 1 + ((le >> 15) & 1u);
-    }
-    const bool lng = le == kLongMark;
-    if (!__ballot(lng)) break;
-    if (lng) {  // the marker step stored one junk symbol at o[-1]
-      const uint32_t lc = resolve_long(S, p, ce, le, maxlen, d, wi, w0, w1, w2);
-      o[-1] = (uint8_t)lc;
-    }
+  while (p < ce) {
+    le = step2(S, p, wi, w0, w1, w2, maxlen, d);
+    o[0] = (uint8_t)le;
+    o[1] = (uint8_t)(le >> 16);
+    o += 1 + ((le >> 15) & 1u);
   }
   P.cnt = (uint32_t)(o - out) - end_pair(le, ce, p);
   P.ex = p;
@@ -742,6 +718,17 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
   uint8_t* const region = S.syms + kCarry + lane * kRegion;
   uint32_t carry = 0, pos0 = 0, entry = 0, err = 0;
   uint64_t S0 = 0, true_pos = 0;
+  // Chunk size: the stream is cut into the fewest segments of at most kSegBits
+  // bits, and each segment evenly over the 64 lanes, so that every segment --
+  // the last one included -- keeps all lanes busy.  A wave's time per segment
+  // follows its longest chunk, so a stream of 1.1 segments at fixed 96-bit
+  // chunks would cost two full segments.
+  uint32_t chunk = kChunk;
+  if (nbits) {
+    const uint64_t nseg = (nbits + kSegBits - 1) / kSegBits;
+    chunk = (uint32_t)((nbits + kWave * nseg - 1) / (kWave * nseg));
+  }
+  const uint32_t segbits = kWave * chunk;
   Fetch16 cur;
   cur.v = make_uint4(0u, 0u, 0u, 0u);
   cur.drop = 16;
@@ -753,20 +740,21 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
     }
     // Next segment's code bytes and this segment's sign/mantissa window go
     // out now and land while the segment decodes.
-    if (S0 + kSegBits < nbits && lane < kStreamLanes)
-      cur = fetch16(st.bits + ((S0 + kSegBits) >> 3) + 16 * lane, bend);
+    if (S0 + segbits < nbits && lane < kStreamLanes)
+      cur = fetch16(st.bits + ((S0 + segbits) >> 3) + 16 * lane, bend);
     SmWin W;
     issue_sm(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
     const uint64_t left = nbits - S0;
-    const uint32_t lim_bits = left < kSegBits ? (uint32_t)left : kSegBits;
-    const uint32_t cs = lane * kChunk;
+    const uint32_t lim_bits = left < segbits ? (uint32_t)left : segbits;
+    const uint32_t cs = lane * chunk;
     const bool active = cs < lim_bits;
-    const uint32_t ce = active ? min(cs + kChunk, lim_bits) : cs;
+    const uint32_t ce = active ? min(cs + chunk, lim_bits) : cs;
     // Lane 0 starts at the true entry; the others kSync bits before their
-    // chunk.  Every lane takes part (decode_chunk has wave-wide votes); an
-    // inactive lane's empty range gives f = ex = cs, cnt = 0.
+    // chunk, or at the entry when that is closer (a true start: small chunks
+    // of a short stream).  An inactive lane's empty range gives f = ex = cs,
+    // cnt = 0.
     Path P;
-    decode_chunk(S, !active ? cs : lane ? cs - kSync : entry, cs, ce, region, maxlen, P);
+    decode_chunk(S, !active ? cs : cs > entry + kSync ? cs - kSync : entry, cs, ce, region, maxlen, P);
     // Resolve: lane i is on the true path when its first start equals its
     // predecessor's exit and the predecessor is.  Lanes that fail re-decode
     // from that exit (rare: a path that did not resynchronise within kSync).
@@ -886,8 +874,8 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
     carry = rem;
     pos0 += take;
     true_pos = S0 + seg_exit;
-    entry = seg_exit - kSegBits;
-    S0 += kSegBits;
+    entry = seg_exit - segbits;
+    S0 += segbits;
   }
   if (!err && (true_pos != nbits || (uint64_t)pos0 + carry != st.count)) err = kErrStream;
   wave_sync();
