@@ -119,8 +119,8 @@ int xksv_cuda_gemv_parallel(const void* input, size_t n, const float* x, float* 
 
 enum { XKSV_CODEC_RAW = 0, XKSV_CODEC_SERIAL = 1, XKSV_CODEC_PARALLEL = 2 };
 
-/* Per-block error bits reported by xksv_hip_plan_errors. */
-enum { XKSV_ERR_HEADER = 1, XKSV_ERR_CODEBOOK = 2, XKSV_ERR_STREAM = 4, XKSV_ERR_SHAPE = 8 };
+/* Per-block error bits reported by xksv_hip_plan_errors (1-8) and xksv_hip_plan_verify (all). */
+enum { XKSV_ERR_HEADER = 1, XKSV_ERR_CODEBOOK = 2, XKSV_ERR_STREAM = 4, XKSV_ERR_SHAPE = 8, XKSV_ERR_DIGEST = 16 };
 
 /* One block of the archive index (src/compile.cpp:461-468 fields). */
 typedef struct xksv_hip_block {
@@ -169,6 +169,25 @@ int xksv_hip_plan_gemm_bf16(xksv_hip_plan* plan, const void* archive, const uint
  * pointers or buffers too small for the plan). */
 int xksv_hip_plan_digests(xksv_hip_plan* plan, const void* out, uint64_t out_size, uint8_t* digests,
                           uint64_t digests_size, void* stream);
+
+/* Block verdicts of an archive verification [src/verify.cpp:239-263]: after
+ * xksv_hip_plan_decode into `out` on the same stream, hash every block's
+ * decoded bytes with SHA-256 on the GPU and compare with `expected` (device,
+ * 32 bytes per block in table order: the index's per-block digests).
+ * verdicts[i] (device, one uint32 per block) = the block's decode error bits,
+ * plus XKSV_ERR_DIGEST when its digest differs; 0 = the block verifies.
+ * Enqueued on `stream`; 0 on success, 1 on error (null pointers or buffers
+ * too small for the plan).  The first call allocates the plan's digest
+ * buffer (32 bytes per block). */
+int xksv_hip_plan_verify(xksv_hip_plan* plan, const void* out, uint64_t out_size, const uint8_t* expected,
+                         uint64_t expected_size, uint32_t* verdicts, void* stream);
+
+/* No reference counterpart: enqueue on `stream` an OR of every block's error
+ * bits from the plan's last decode or GEMM into *flags (a device word the
+ * caller owns and clears; the bits accumulate across calls).  No host
+ * synchronisation, so a forward pass can record errors under graph capture
+ * and check them later.  0 on success, 1 on error. */
+int xksv_hip_plan_error_flags(xksv_hip_plan* plan, uint32_t* flags, void* stream);
 
 /* Synchronize `stream`, return the number of failed blocks (or -1 on a HIP
  * error); *first_bad (optional) gets the first failing block index or -1,

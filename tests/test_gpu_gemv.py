@@ -36,7 +36,7 @@ def test_serial_gemv(hip, oracle, rows, cols):
     np.testing.assert_allclose(y.cpu().numpy(), want, atol=1e-5, rtol=1e-5)
 
 
-@pytest.mark.parametrize("rows,cols,batch", [(3, 7, 2), (17, 33, 4), (16, 512, 5), (16, 256, 16), (16, 128, 37)])
+@pytest.mark.parametrize("rows,cols,batch", [(3, 7, 2), (17, 33, 4), (16, 512, 5), (16, 256, 16), (16, 256, 17), (16, 128, 37)])
 def test_serial_gemm(hip, oracle, rows, cols, batch):
     """tests/test_cuda.py:35-43: X [cols, batch], Y [rows, batch] row-major fp32."""
     w = gen({"kind": "normal", "seed": 3 + batch, "shape": [rows, cols]})
@@ -64,7 +64,7 @@ def test_parallel_gemv(hip, oracle, rows, cols):
     assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("batch", [2, 4, 8, 16, 20])
+@pytest.mark.parametrize("batch", [2, 4, 8, 16, 17, 20, 33])
 def test_parallel_gemm(hip, oracle, batch):
     rows, cols = 16, 4096
     w = gen({"kind": "normal", "seed": 100 + batch, "shape": [rows, cols]})

@@ -72,8 +72,58 @@ def test_resident_linear_reports_corrupt_blocks(hip):
     rl = xksv_torch.ResidentLinear.from_linear(hip, lin, 2)
     first = int(rl._decode_table[0]["offset"])
     rl.archive[first] ^= 1  # XKSP2 magic of block 0
+    rl(torch.randn(1, 4096, device="cuda"))  # recorded on the device, no host sync
     with pytest.raises(xksv_hip.XksvError):
-        rl(torch.randn(1, 4096, device="cuda"))
+        rl.check_errors()
+    rl.check = True
+    with pytest.raises(xksv_hip.XksvError):
+        rl(torch.randn(2, 4096, device="cuda", dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("tokens", [1, 5])
+@torch.no_grad()
+def test_resident_linear_fp32_activations(hip, tokens):
+    """fp32 activations take the fp32-X path (the reference's fused GEMV numerics,
+    python/runtime.py:267): rel-L2 <= 1e-5 against fp64 with the unrounded fp32 x."""
+    torch.manual_seed(40 + tokens)
+    lin = torch.nn.Linear(4096, 384, bias=True, device="cuda", dtype=torch.bfloat16)
+    torch.nn.init.normal_(lin.weight, std=0.02)
+    rl = xksv_torch.ResidentLinear.from_linear(hip, lin, 2)
+    x = torch.randn(tokens, 4096, device="cuda", dtype=torch.float32)
+    want = x.double() @ lin.weight.double().T + lin.bias.double()
+    y = rl(x)
+    assert y.dtype == torch.float32
+    assert _rel_l2(y.cpu(), want.cpu()) <= 1e-5
+    rl.check_errors()
+
+
+@torch.no_grad()
+def test_resident_linear_forward_under_graph_capture(hip):
+    """forward issues no host synchronisation: it captures into a HIP graph, and
+    every replay (with eager work and synchronisations between replays) equals
+    the eager result bit for bit, for the fp32 and the bf16 (MFMA) paths."""
+    torch.manual_seed(77)
+    lin = torch.nn.Linear(4096, 256, bias=False, device="cuda", dtype=torch.bfloat16)
+    torch.nn.init.normal_(lin.weight, std=0.02)
+    rl = xksv_torch.ResidentLinear.from_linear(hip, lin, 2)
+    xs = {torch.float32: torch.randn(3, 4096, device="cuda"),
+          torch.bfloat16: torch.randn(8, 4096, device="cuda").to(torch.bfloat16)}
+    for dt, x in xs.items():
+        eager = rl(x).clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            rl(x)  # warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            y = rl(x)
+        for i in range(3):
+            x.add_(0)  # eager work between replays
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, eager), (dt, i)
+    rl.check_errors()
 
 
 def test_tiny_llama_logits_with_resident_layers(hip):

@@ -273,6 +273,7 @@ struct xksv_hip_plan {
   bool tile_parallel = false;  // parallel32 slabs split into whole-tile substreams (MFMA consumer)
   uint8_t* scratch = nullptr;
   uint8_t* item_mem = nullptr;  // ItemScratch of the fused XKSP2 list (none: workgroup-per-block kernels)
+  uint8_t* digests = nullptr;   // verification: SHA-256 per block, table order (allocated on first use)
   ItemScratch items{};
   std::vector<uint32_t> h_status;
 };
@@ -531,7 +532,7 @@ int xksv_hip_plan_destroy(xksv_hip_plan* P) {
   if (P->device >= 0 && cur != P->device) (void)hipSetDevice(P->device);
   for (void* p : {(void*)P->d_serial, (void*)P->d_parallel, (void*)P->d_raw, (void*)P->status, (void*)P->g_fserial,
                   (void*)P->g_fparallel, (void*)P->g_gser, (void*)P->g_gpar, (void*)P->g_gplain, (void*)P->g_raw,
-                  (void*)P->scratch, (void*)P->item_mem})
+                  (void*)P->scratch, (void*)P->item_mem, (void*)P->digests})
     if (p) (void)hipFree(p);
   if (cur >= 0 && cur != P->device) (void)hipSetDevice(cur);
   delete P;
@@ -630,6 +631,27 @@ int xksv_hip_plan_digests(xksv_hip_plan* P, const void* out, uint64_t out_size, 
                  launch_sha256_blocks(P->d_raw, P->n_raw, o, digests, s) != hipSuccess
              ? 1
              : 0;
+}
+
+int xksv_hip_plan_verify(xksv_hip_plan* P, const void* out, uint64_t out_size, const uint8_t* expected,
+                         uint64_t expected_size, uint32_t* verdicts, void* stream) {
+  if (!P || !out || !expected || !verdicts || out_size < P->out_extent || expected_size < 32ull * P->blocks.size())
+    return 1;
+  if (P->blocks.empty()) return 0;
+  if (!P->digests && hipMalloc(reinterpret_cast<void**>(&P->digests), 32 * P->blocks.size()) != hipSuccess) return 1;
+  if (xksv_hip_plan_digests(P, out, out_size, P->digests, 32 * P->blocks.size(), stream)) return 1;
+  return launch_digest_verdicts(P->digests, expected, P->status, (uint32_t)P->blocks.size(), verdicts,
+                                static_cast<hipStream_t>(stream)) == hipSuccess
+             ? 0
+             : 1;
+}
+
+int xksv_hip_plan_error_flags(xksv_hip_plan* P, uint32_t* flags, void* stream) {
+  if (!P || !flags) return 1;
+  return launch_or_status(P->status, (uint32_t)P->blocks.size(), flags, static_cast<hipStream_t>(stream)) ==
+                 hipSuccess
+             ? 0
+             : 1;
 }
 
 int64_t xksv_hip_plan_errors(xksv_hip_plan* P, void* stream, int64_t* first_bad, uint32_t* bits) {

@@ -70,6 +70,8 @@ hipError_t launch_gemm_plain(const DevBlock* blocks, uint32_t nblocks, const uin
 hipError_t launch_gemm_plain_bf16(const DevBlock* blocks, uint32_t nblocks, const uint8_t* base, const uint16_t* x,
                                   uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t s);
+// *flags |= OR of status[0 .. n) (vector atomic), enqueued on s.
+hipError_t launch_or_status(const uint32_t* status, uint32_t n, uint32_t* flags, hipStream_t s);
 // flags[i] for XKSP2 block i: bit 0 = substreams on 8-element boundaries
 // (fused consumers apply), bit 1 = on whole tiles (MFMA applies); both bits
 // for a header that does not parse (the fused kernels report it).
@@ -79,5 +81,8 @@ hipError_t launch_route_parallel(const DevBlock* blocks, uint32_t n, const uint8
 // digests[32 * status_slot] (xksv_sha256.hip).
 hipError_t launch_sha256_blocks(const DevBlock* blocks, uint32_t nblocks, const uint8_t* out, uint8_t* digests,
                                 hipStream_t s);
+// verdicts[i] = status[i] | kErrDigest when digests[32 i ..] != expected[32 i ..].
+hipError_t launch_digest_verdicts(const uint8_t* digests, const uint8_t* expected, const uint32_t* status, uint32_t n,
+                                  uint32_t* verdicts, hipStream_t s);
 
 }  // namespace xksv

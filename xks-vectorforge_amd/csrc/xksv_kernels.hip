@@ -1760,6 +1760,14 @@ __global__ void __launch_bounds__(256) k_route_parallel(const DevBlock* __restri
   }
 }
 
+// OR of n status words into *flags (a sticky device word the caller owns).
+__global__ void __launch_bounds__(256) k_or_status(const uint32_t* __restrict__ status, uint32_t n,
+                                                   uint32_t* __restrict__ flags) {
+  uint32_t v = 0;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) v |= status[i];
+  if (v) atomicOr(flags, v);
+}
+
 __global__ void k_fill_u32(uint32_t* p, uint64_t n, uint32_t v) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
     p[i] = v;
@@ -1843,7 +1851,11 @@ hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t co
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
                            const ItemScratch* is, unsigned cus, hipStream_t s) {
   if (!nblocks) return hipSuccess;
-  gemm_valu<GemmF32>(s, blocks, nblocks, codec, arc, GemmArgs{x, ldx, nb, y, ldy}, status, is, cus);
+  const GemmArgs ga{x, ldx, nb, y, ldy};
+  // GemmF32<1> reads x as a contiguous vector; a one-column group of a wider
+  // X (the last group of a batch of 16 k + 1) takes the strided consumer.
+  if (nb == 1 && ldx != 1) gemm_any<GemmF32<4>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
+  else gemm_valu<GemmF32>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   return hipGetLastError();
 }
 
@@ -1885,6 +1897,13 @@ hipError_t launch_route_parallel(const DevBlock* blocks, uint32_t n, const uint8
   if (!n) return hipSuccess;
   const unsigned g = (n + 255) / 256;
   hipLaunchKernelGGL(k_route_parallel, dim3(g < 1024 ? g : 1024u), dim3(256), 0, s, blocks, n, arc, flags);
+  return hipGetLastError();
+}
+
+hipError_t launch_or_status(const uint32_t* status, uint32_t n, uint32_t* flags, hipStream_t s) {
+  if (!n) return hipSuccess;
+  const unsigned g = (n + 255) / 256;
+  hipLaunchKernelGGL(k_or_status, dim3(g < 64 ? g : 64u), dim3(256), 0, s, status, n, flags);
   return hipGetLastError();
 }
 

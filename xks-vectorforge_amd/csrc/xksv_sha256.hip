@@ -131,7 +131,37 @@ __global__ void __launch_bounds__(256) k_sha256_blocks(const DevBlock* __restric
   for (int i = 0; i < 8; ++i) dg[i] = be32(h[i]);
 }
 
+// Per-block verdict of a verification pass: the block's decode error bits
+// plus kErrDigest when the SHA-256 of its decoded bytes differs from the
+// digest the index records for it [src/verify.cpp:262-263].  Digests, the
+// expected digests and the status words are indexed by block (table order).
+__global__ void __launch_bounds__(256) k_digest_verdicts(const uint8_t* __restrict__ digests,
+                                                         const uint8_t* __restrict__ expected,
+                                                         const uint32_t* __restrict__ status, uint32_t n,
+                                                         uint32_t* __restrict__ verdicts) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    uint32_t diff = 0;
+#pragma unroll
+    for (int k = 0; k < 32; k += 4) {
+      uint32_t a, b;
+      __builtin_memcpy(&a, digests + 32ull * i + k, 4);
+      __builtin_memcpy(&b, expected + 32ull * i + k, 4);
+      diff |= a ^ b;
+    }
+    verdicts[i] = status[i] | (diff ? (uint32_t)kErrDigest : 0u);
+  }
+}
+
 }  // namespace
+
+hipError_t launch_digest_verdicts(const uint8_t* digests, const uint8_t* expected, const uint32_t* status, uint32_t n,
+                                  uint32_t* verdicts, hipStream_t s) {
+  if (!n) return hipSuccess;
+  const unsigned g = (n + 255) / 256;
+  hipLaunchKernelGGL(k_digest_verdicts, dim3(g < 1024 ? g : 1024u), dim3(256), 0, s, digests, expected, status, n,
+                     verdicts);
+  return hipGetLastError();
+}
 
 hipError_t launch_sha256_blocks(const DevBlock* blocks, uint32_t nblocks, const uint8_t* out, uint8_t* digests,
                                 hipStream_t s) {

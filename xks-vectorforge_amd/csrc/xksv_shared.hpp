@@ -18,6 +18,7 @@ enum Err : uint32_t {
   kErrCodebook = 2,  // oversubscribed canonical code lengths
   kErrStream = 4,    // invalid code, truncated stream, trailing bits, or count mismatch
   kErrShape = 8,     // header shape disagrees with the descriptor, or exceeds device limits
+  kErrDigest = 16,   // decoded bytes' SHA-256 differs from the index digest (verification)
 };
 
 // One encoded block as the kernels see it (device memory).  `src` and `size`

@@ -23,7 +23,7 @@ LIB_PATH = Path(os.environ.get("XKSV_HIP_LIBRARY", HERE / "libxksv_hip.so"))
 
 CODEC_RAW, CODEC_SERIAL, CODEC_PARALLEL = 0, 1, 2
 CODEC_NAMES = {"raw": CODEC_RAW, "bf16-huffman-tile16": CODEC_SERIAL, "bf16-huffman-parallel32": CODEC_PARALLEL}
-ERR_HEADER, ERR_CODEBOOK, ERR_STREAM, ERR_SHAPE = 1, 2, 4, 8
+ERR_HEADER, ERR_CODEBOOK, ERR_STREAM, ERR_SHAPE, ERR_DIGEST = 1, 2, 4, 8, 16
 
 
 class Block(ctypes.Structure):
@@ -66,6 +66,8 @@ _SIGNATURES = {
     "xksv_hip_plan_gemm_bf16": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "xksv_hip_plan_errors": (ctypes.c_int64, [_vp, _vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(_u32)]),
     "xksv_hip_plan_digests": (ctypes.c_int, [_vp, _vp, _u64, _vp, _u64, _vp]),
+    "xksv_hip_plan_verify": (ctypes.c_int, [_vp, _vp, _u64, _vp, _u64, _vp, _vp]),
+    "xksv_hip_plan_error_flags": (ctypes.c_int, [_vp, _vp, _vp]),
     "xksv_encode_tensor": (_int, [_vp, _u64, _int, _u64, _u32, _u32, _pvp, ctypes.POINTER(_u64),
                                   ctypes.POINTER(ctypes.POINTER(Block)), ctypes.POINTER(_u64)]),
     "xksv_hip_version": (_int, []),
@@ -224,6 +226,20 @@ class Plan:
         if self.lib.lib.xksv_hip_plan_digests(self.handle, out_ptr, out_size, digests_ptr, digests_size,
                                               stream or None):
             raise XksvError("xksv_hip_plan_digests failed to launch")
+
+    def verify(self, out_ptr: int, out_size: int, expected_ptr: int, expected_size: int, verdicts_ptr: int,
+               stream: int = 0) -> None:
+        """Per-block verdicts (device uint32 per block) of the last decode into `out`:
+        decode error bits, plus ERR_DIGEST where the block's SHA-256 differs from
+        `expected` (device, 32 bytes per block in table order)."""
+        if self.lib.lib.xksv_hip_plan_verify(self.handle, out_ptr, out_size, expected_ptr, expected_size,
+                                             verdicts_ptr, stream or None):
+            raise XksvError("xksv_hip_plan_verify failed to launch")
+
+    def error_flags(self, flags_ptr: int, stream: int = 0) -> None:
+        """Enqueue *flags (device uint32) |= OR of the last call's block error bits; no host sync."""
+        if self.lib.lib.xksv_hip_plan_error_flags(self.handle, flags_ptr, stream or None):
+            raise XksvError("xksv_hip_plan_error_flags failed to launch")
 
     def errors(self, stream: int = 0):
         """(number of failed blocks, first failing block or -1, OR of error bits)."""

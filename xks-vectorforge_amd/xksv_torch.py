@@ -9,15 +9,23 @@ input shape falls back to `F.linear` on decoded weights.  Its GPU-decode load
 into the parameter's storage.
 
 Here the blocks of a layer stay resident in HBM and one plan call runs the
-fused decode-GEMM for the whole layer and any batch: the input is taken as
-bf16 X [tokens, in_features] (the layout of x @ W.T) and the product is
-accumulated in fp32 (bf16 MFMA from 8 tokens, fp32 FMAs below).  The weight
-is never materialised.  `ResidentLinear.decode_weight` and
-`decode_into` are the GPU-decode load.
+fused decode-GEMM for the whole layer and any batch.  The weight is never
+materialised.  Activations pick the path:
+  * fp32 (and fp16) inputs take the fp32-X path, the reference's own numerics
+    (fp32 x, fp32 accumulation, python/runtime.py:267): each output is the
+    fp32 sum of exact products, rel-L2 <= 1e-5 against fp64;
+  * bf16 inputs take the bf16-X path in the layout of x @ W.T (bf16 MFMA
+    from 8 tokens, fp32 FMAs below), fp32 accumulation.
+`ResidentLinear.decode_weight` / `decode_into` are the GPU-decode load, and
+`from_archive` builds the layer from an .xksv archive's blocks.
 
-Numerics: each output is the fp32 sum of exact products of bf16 weights and
-bf16 activations, so the result differs from torch's bf16 `F.linear` only by
-the final rounding to the activation dtype and by summation order (the
+A forward pass never synchronises the host: block errors are ORed into a
+sticky device word (`xksv_hip_plan_error_flags`) that `check_errors()` reads,
+so a forward can run under HIP graph capture.  `check=True` restores a
+synchronous check after every forward.
+
+Numerics of the bf16 path differ from torch's bf16 `F.linear` only by the
+final rounding to the activation dtype and by summation order (the
 reference's own fused path is likewise allowed to differ: its test bounds the
 logits by atol = rtol = 0.03, tests/test_stream.py:54-62).
 """
@@ -47,7 +55,7 @@ class ResidentLinear(torch.nn.Module):
 
     def __init__(self, lib: xksv_hip.Library, enc: np.ndarray, table: np.ndarray, out_features: int,
                  in_features: int, bias: torch.Tensor | None = None, device: str | torch.device = "cuda",
-                 check: bool = True):
+                 check: bool = False):
         super().__init__()
         self.lib = lib
         self.in_features, self.out_features = int(in_features), int(out_features)
@@ -62,10 +70,31 @@ class ResidentLinear(torch.nn.Module):
         self.plan = xksv_hip.Plan(lib, gemm_table, self.archive.numel())
         self._decode_plan = None
         self.bias = None if bias is None else torch.nn.Parameter(bias.detach().clone(), requires_grad=False)
+        self._errors = torch.zeros(1, dtype=torch.int32, device=self.archive.device)  # sticky XKSV_ERR_* bits
+        # The first GEMM call prepares the plan's routing (one synchronisation):
+        # do it here, so that forward never synchronises.
+        x0 = torch.zeros(self.in_features, dtype=torch.float32, device=self.archive.device)
+        y0 = torch.empty(self.out_features, dtype=torch.float32, device=self.archive.device)
+        stream = torch.cuda.current_stream(self.archive.device).cuda_stream
+        self.plan.gemm(self.archive.data_ptr(), x0.data_ptr(), 1, y0.data_ptr(), stream)
+        self.plan.error_flags(self._errors.data_ptr(), stream)
+
+    @classmethod
+    def from_archive(cls, lib: xksv_hip.Library, archive, name: str, bias: torch.Tensor | None = None,
+                     device: str | torch.device = "cuda", check: bool = False) -> "ResidentLinear":
+        """A 2-D BF16 tensor of an .xksv archive (path or xksv_archive.Archive), its blocks
+        -- compressed and raw, as the index lists them -- copied to HBM once."""
+        import xksv_archive
+        arc = archive if isinstance(archive, xksv_archive.Archive) else xksv_archive.Archive(archive)
+        t = arc.tensors.get(name)
+        if t is None or t["dtype"] != "BF16" or len(t["shape"]) != 2:
+            raise ValueError(f"{name} is not a 2-D BF16 tensor of the archive")
+        table, lo, hi, _, _ = arc.block_table([name])
+        return cls(lib, np.array(arc.read(lo, hi - lo)), table, t["shape"][0], t["shape"][1], bias, device, check)
 
     @classmethod
     def from_linear(cls, lib: xksv_hip.Library, linear: torch.nn.Linear, codec: int = CODEC_PARALLEL,
-                    check: bool = True) -> "ResidentLinear":
+                    check: bool = False) -> "ResidentLinear":
         """Encode `linear.weight` (bf16) with the slab rule and keep the blocks in HBM."""
         w = linear.weight
         if w.dim() != 2:
@@ -77,19 +106,36 @@ class ResidentLinear(torch.nn.Module):
         if x.shape[-1] != self.in_features:
             raise ValueError(f"expected last dimension {self.in_features}, got {x.shape[-1]}")
         lead = x.shape[:-1]
-        xb = x.reshape(-1, self.in_features).to(torch.bfloat16).contiguous()
-        batch = xb.shape[0]
-        y = torch.empty(batch, self.out_features, dtype=torch.float32, device=xb.device)
+        x2 = x.reshape(-1, self.in_features)
+        batch = x2.shape[0]
+        if x.dtype == torch.bfloat16:
+            xb = x2.contiguous()
+            y = torch.empty(batch, self.out_features, dtype=torch.float32, device=x.device)
+        else:  # fp32 X [in_features, batch], Y [out_features, batch] (cuda/decode.cu:94 layout)
+            xb = x2.float().t().contiguous() if batch > 1 else x2.float().contiguous()
+            y = torch.empty(self.out_features, batch, dtype=torch.float32, device=x.device)
         if batch:
-            stream = torch.cuda.current_stream(xb.device).cuda_stream
-            self.plan.gemm_bf16(self.archive.data_ptr(), xb.data_ptr(), batch, y.data_ptr(), stream)
+            stream = torch.cuda.current_stream(x.device).cuda_stream
+            if x.dtype == torch.bfloat16:
+                self.plan.gemm_bf16(self.archive.data_ptr(), xb.data_ptr(), batch, y.data_ptr(), stream)
+            else:
+                self.plan.gemm(self.archive.data_ptr(), xb.data_ptr(), batch, y.data_ptr(), stream)
+            self.plan.error_flags(self._errors.data_ptr(), stream)
             if self.check:
-                n, first, bits = self.plan.errors(stream)
-                if n:
-                    raise xksv_hip.XksvError(f"fused decode-GEMM failed on block {first} (error bits {bits:#x})")
+                self.check_errors()
+        if x.dtype != torch.bfloat16:
+            y = y.t()
         if self.bias is not None:
-            y += self.bias.float()
+            y = y + self.bias.float()
         return y.to(x.dtype).reshape(*lead, self.out_features)
+
+    def check_errors(self) -> None:
+        """Raise XksvError if any forward so far met a block that failed to decode
+        (synchronises the current stream); the record is then cleared."""
+        bits = int(self._errors.item())
+        if bits:
+            self._errors.zero_()
+            raise xksv_hip.XksvError(f"fused decode-GEMM met a corrupt block (error bits {bits:#x})")
 
     def _decoder(self) -> xksv_hip.Plan:
         if self._decode_plan is None:
@@ -119,17 +165,31 @@ class ResidentLinear(torch.nn.Module):
 
 def install_resident_linear(model: torch.nn.Module, lib: xksv_hip.Library | None = None,
                             codec: int = CODEC_PARALLEL, skip: tuple[str, ...] = ("lm_head",),
-                            check: bool = True) -> int:
+                            check: bool = False, archive=None) -> int:
     """Replace the bf16 2-D `nn.Linear` layers of `model` (except names in
     `skip`) by ResidentLinear; returns how many were replaced.  Mirrors the
     layer selection of python/runtime.py:253-261 (bf16 weights, no lm_head);
-    layers with a bias are kept resident too and add it after the GEMM."""
+    layers with a bias are kept resident too and add it after the GEMM.  With
+    `archive` (path or Archive), each layer's blocks come from the archive's
+    `<name>.weight` tensor instead of encoding the module's weight."""
     lib = lib or xksv_hip.Library()
     targets = [(name, m) for name, m in model.named_modules()
                if isinstance(m, torch.nn.Linear) and name.split(".")[-1] not in skip and name not in skip
                and m.weight.dtype == torch.bfloat16 and m.weight.dim() == 2]
+    if archive is not None:
+        import xksv_archive
+        archive = archive if isinstance(archive, xksv_archive.Archive) else xksv_archive.Archive(archive)
+    done = 0
     for name, m in targets:
         parent_name, _, leaf = name.rpartition(".")
         parent = model.get_submodule(parent_name) if parent_name else model
-        setattr(parent, leaf, ResidentLinear.from_linear(lib, m, codec, check))
-    return len(targets)
+        if archive is not None:  # the layer's blocks from the archive, as python/runtime.py:253-261 selects them
+            t = archive.tensors.get(name + ".weight")
+            if t is None or t["dtype"] != "BF16" or list(t["shape"]) != list(m.weight.shape):
+                continue
+            layer = ResidentLinear.from_archive(lib, archive, name + ".weight", m.bias, m.weight.device, check)
+        else:
+            layer = ResidentLinear.from_linear(lib, m, codec, check)
+        setattr(parent, leaf, layer)
+        done += 1
+    return done
