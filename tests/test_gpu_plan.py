@@ -226,3 +226,93 @@ def test_plan_gemm_nonstandard_chunk_counts(hip, oracle, batch):
         assert np.linalg.norm(yb.cpu().numpy() - want) / np.linalg.norm(want) <= 2e-3
     finally:
         plan.close()
+
+
+def _gemv(plan, d_arc, x, rows):
+    y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+    plan.gemm(d_arc.data_ptr(), x.data_ptr(), 1, y.data_ptr())
+    return y, plan.errors()
+
+
+def test_plan_gemv_index_across_archives(hip, oracle):
+    """The fused GEMV's codeword index is built from the archive of the first GEMM call
+    and checked on every use.  Same table, other archives:
+    * sign-flipped weights (same code bits, so the index still holds): y is exact;
+    * code bits changed after the index was built (a stale index): the changed
+      segment does not chain and decodes speculatively, so a block the oracle
+      rejects is reported and a block the oracle decodes differently gives the GEMV
+      of the oracle's weights."""
+    rows, cols = 64, 4096
+    w = syn.normal_bf16(4242, (rows, cols))
+    enc, table = hip.encode_tensor(w, 2)
+    table = table.copy()
+    table["out_offset"] //= cols * 2
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    x = torch.randn(cols, dtype=torch.float32, device="cuda")
+    xd = x.cpu().numpy().astype(np.float64)
+    try:
+        y, errs = _gemv(plan, _upload(enc), x, rows)  # builds the index
+        assert errs[0] == 0
+        assert np.linalg.norm(y.cpu().numpy() - oracle.gemm_f64(w, xd)) <= 1e-5 * np.linalg.norm(oracle.gemm_f64(w, xd))
+        wn = w ^ np.uint16(0x8000)
+        enc_n, table_n = hip.encode_tensor(wn, 2)
+        assert enc_n.nbytes == enc.nbytes and np.array_equal(table_n["size"], table["size"])
+        yn, errs = _gemv(plan, _upload(enc_n), x, rows)
+        assert errs[0] == 0 and torch.equal(yn, -y)
+
+        # code bits of block 1, last substream: one flip the oracle rejects, one it accepts
+        t = table[1]
+        blob = enc[int(t["offset"]):int(t["offset"] + t["size"])].tobytes()
+        rejected = accepted = None
+        for back in range(2, 600):
+            for bit in range(8):
+                b = bytearray(blob)
+                b[len(b) - back] ^= 1 << bit
+                rc, dec = oracle.unpack_parallel(bytes(b))
+                if rc and rejected is None:
+                    rejected = (back, bit)
+                if rc == 0 and dec != blob and accepted is None and dec != raw_bytes(w[16:32]):
+                    accepted = (back, bit, dec)
+            if rejected and accepted:
+                break
+        assert rejected is not None
+        enc_r = enc.copy()
+        enc_r[int(t["offset"] + t["size"]) - rejected[0]] ^= 1 << rejected[1]
+        yr, errs = _gemv(plan, _upload(enc_r), x, rows)
+        assert errs[:2] == (1, 1) and errs[2] == xksv_hip.ERR_STREAM
+        keep = np.r_[0:16, 32:64]
+        assert torch.equal(yr[keep], y[keep])
+        if accepted is not None:
+            back, bit, dec = accepted
+            enc_a = enc.copy()
+            enc_a[int(t["offset"] + t["size"]) - back] ^= 1 << bit
+            ya, errs = _gemv(plan, _upload(enc_a), x, rows)
+            assert errs[0] == 0
+            wa = w.copy()
+            wa[16:32] = np.frombuffer(dec, np.uint16).reshape(16, cols)
+            want = oracle.gemm_f64(wa, xd)
+            assert np.linalg.norm(ya.cpu().numpy() - want) <= 1e-5 * np.linalg.norm(want)
+    finally:
+        plan.close()
+
+
+def test_plan_gemv_unindexed_items(hip, oracle):
+    """Substreams whose segments are too long for the index (high-entropy exponents:
+    about 6 bits per code) take the speculative path; y matches fp64."""
+    rows, cols = 32, 4096
+    rng = np.random.default_rng(77)
+    w = ((rng.integers(64, 128, rows * cols, dtype=np.uint32) << 7) | rng.integers(0, 256, rows * cols, dtype=np.uint32))
+    w = w.astype(np.uint16).reshape(rows, cols)
+    enc, table = hip.encode_tensor(w, 2)
+    assert set(table["codec"]) == {xksv_hip.CODEC_PARALLEL}
+    table = table.copy()
+    table["out_offset"] //= cols * 2
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    try:
+        x = torch.randn(cols, dtype=torch.float32, device="cuda")
+        y, errs = _gemv(plan, _upload(enc), x, rows)
+        assert errs[0] == 0
+        want = oracle.gemm_f64(w, x.cpu().numpy().astype(np.float64))
+        assert np.linalg.norm(y.cpu().numpy() - want) <= 1e-5 * np.linalg.norm(want)
+    finally:
+        plan.close()

@@ -274,6 +274,8 @@ struct xksv_hip_plan {
   uint8_t* scratch = nullptr;
   uint8_t* item_mem = nullptr;  // ItemScratch of the fused XKSP2 list (none: workgroup-per-block kernels)
   uint8_t* digests = nullptr;   // verification: SHA-256 per block, table order (allocated on first use)
+  uint16_t* index = nullptr;    // codeword index of the fused XKSP2 items (ItemScratch::index)
+  uint64_t index_bytes = 0;
   ItemScratch items{};
   std::vector<uint32_t> h_status;
 };
@@ -374,6 +376,17 @@ bool prepare_gemm(xksv_hip_plan* P, const uint8_t* arc, hipStream_t s) {
     if (hipMalloc(reinterpret_cast<void**>(&P->item_mem), item_bytes) != hipSuccess) return false;
     P->items.partial = reinterpret_cast<float*>(P->item_mem);
     P->items.done = reinterpret_cast<uint32_t*>(P->item_mem + (uint64_t)P->n_fparallel * (kItemScratchPerBlock - 4));
+    // Codeword index of the items (weights are static: built once, here, from
+    // the archive of the first GEMM call; the kernels check it as they use it).
+    // Sized for the slab rule's 32 substreams of 16 * cols / 32 symbols; an
+    // item with more symbols is decoded speculatively.
+    const uint64_t syms = (16 * cols + kMaxChunks - 1) / kMaxChunks;
+    const uint32_t segs = (uint32_t)std::max<uint64_t>(1, (syms + kIdxSegSyms - 1) / kIdxSegSyms);
+    P->index_bytes = (uint64_t)P->n_fparallel * kMaxChunks * segs * 64 * sizeof(uint16_t);
+    if (hipMalloc(reinterpret_cast<void**>(&P->index), P->index_bytes) != hipSuccess) return false;
+    if (launch_index_items(P->g_fparallel, P->n_fparallel, arc, P->index, segs, s) != hipSuccess) return false;
+    P->items.index = P->index;
+    P->items.index_segs = segs;
   }
   P->gemm_valid = true;
   return true;
@@ -532,7 +545,7 @@ int xksv_hip_plan_destroy(xksv_hip_plan* P) {
   if (P->device >= 0 && cur != P->device) (void)hipSetDevice(P->device);
   for (void* p : {(void*)P->d_serial, (void*)P->d_parallel, (void*)P->d_raw, (void*)P->status, (void*)P->g_fserial,
                   (void*)P->g_fparallel, (void*)P->g_gser, (void*)P->g_gpar, (void*)P->g_gplain, (void*)P->g_raw,
-                  (void*)P->scratch, (void*)P->item_mem, (void*)P->digests})
+                  (void*)P->scratch, (void*)P->item_mem, (void*)P->digests, (void*)P->index})
     if (p) (void)hipFree(p);
   if (cur >= 0 && cur != P->device) (void)hipSetDevice(cur);
   delete P;

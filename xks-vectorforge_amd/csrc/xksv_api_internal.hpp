@@ -70,6 +70,10 @@ hipError_t launch_gemm_plain(const DevBlock* blocks, uint32_t nblocks, const uin
 hipError_t launch_gemm_plain_bf16(const DevBlock* blocks, uint32_t nblocks, const uint8_t* base, const uint16_t* x,
                                   uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t s);
+// Codeword index (ItemScratch::index) of the fused XKSP2 items of `blocks`:
+// `segs` segments of 64 u16 entries per item.
+hipError_t launch_index_items(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint16_t* index,
+                              uint32_t segs, hipStream_t s);
 // *flags |= OR of status[0 .. n) (vector atomic), enqueued on s.
 hipError_t launch_or_status(const uint32_t* status, uint32_t n, uint32_t* flags, hipStream_t s);
 // flags[i] for XKSP2 block i: bit 0 = substreams on 8-element boundaries

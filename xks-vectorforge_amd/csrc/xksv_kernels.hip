@@ -48,6 +48,11 @@ constexpr uint32_t kLongMark = kLongLen << 8;
 constexpr uint32_t kMaxLenFast = 32;
 constexpr uint32_t kSlowSeg = 4096;                 // symbols per bit-serial segment (multiple of 256)
 constexpr uint64_t kMagicXKSP2 = 0x0000003250534B58ull;  // "XKSP2\0\0\0" little-endian
+// Longest segment of an indexed item (fused GEMM codeword index), in code
+// bits: the segment, its start's bit offset within its first byte, the
+// register window's lookahead (96 bits) and a dead path's jump (kLongLen)
+// stay inside the 6,272 staged bits.
+constexpr uint32_t kIdxMaxSpan = kStreamLanes * 128 - 7 - 96 - kLongLen - 32;
 
 // Every function that takes the LDS block by reference is force-inlined: the
 // compiler then addresses it with DS instructions.  Through a call it would
@@ -710,34 +715,44 @@ __device__ __forceinline__ void stage_inputs(Smem& S, uint32_t lane, const Strea
 // exponents in stream order.  `first` holds the stream's first 784 code
 // bytes; later segments are loaded one segment ahead.  Returns error bits.
 template <class Cons>
+//
+// `start_bit` / `start_pos` resume the stream at a codeword boundary already
+// known to be true (its symbol index start_pos, a multiple of 256): the
+// indexed path hands a stream over here when its index does not chain.  A
+// stream decoded from its start has its first bytes staged with its inputs.
 __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen,
-                                                const uint8_t* blk_end, Cons& C, const StreamIn& PN, bool next) {
+                                                const uint8_t* blk_end, Cons& C, const StreamIn& PN, bool next,
+                                                uint64_t start_bit = 0, uint32_t start_pos = 0) {
   const uint64_t nbits = st.nbits;
   const uint8_t* bend = st.bits + ((nbits + 7) >> 3);
   if (bend > blk_end) bend = blk_end;
   uint8_t* const region = S.syms + kCarry + lane * kRegion;
-  uint32_t carry = 0, pos0 = 0, entry = 0, err = 0;
-  uint64_t S0 = 0, true_pos = 0;
+  uint64_t S0 = start_bit & ~7ull, true_pos = start_bit;
+  uint32_t carry = 0, pos0 = start_pos, entry = (uint32_t)(start_bit - S0), err = 0;
   // Chunk size: the stream is cut into the fewest segments of at most kSegBits
   // bits, and each segment evenly over the 64 lanes, so that every segment --
   // the last one included -- keeps all lanes busy.  A wave's time per segment
   // follows its longest chunk, so a stream of 1.1 segments at fixed 96-bit
   // chunks would cost two full segments.
   uint32_t chunk = kChunk;
-  if (nbits) {
-    const uint64_t nseg = (nbits + kSegBits - 1) / kSegBits;
-    chunk = (uint32_t)((nbits + kWave * nseg - 1) / (kWave * nseg));
+  if (nbits > S0) {
+    const uint64_t nseg = (nbits - S0 + kSegBits - 1) / kSegBits;
+    chunk = (uint32_t)((nbits - S0 + kWave * nseg - 1) / (kWave * nseg));
   }
   const uint32_t segbits = kWave * chunk;
   Fetch16 cur;
   cur.v = make_uint4(0u, 0u, 0u, 0u);
   cur.drop = 16;
+  const bool resume = start_bit != 0 || start_pos != 0;
+  if (resume && lane < kStreamLanes) cur = fetch16(st.bits + (S0 >> 3) + 16 * lane, bend);
+  bool stage_top = resume;
   bool staged = false;
   while (true_pos < nbits) {
-    if (S0) {  // the first segment's bytes were staged with the stream's inputs
+    if (stage_top) {  // a stream's first segment was staged with its inputs
       stage_bits(S, lane, cur.value());
       wave_sync();
     }
+    stage_top = true;
     // Next segment's code bytes and this segment's sign/mantissa window go
     // out now and land while the segment decodes.
     if (S0 + segbits < nbits && lane < kStreamLanes)
@@ -886,6 +901,112 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
   return err;
 }
 
+// Decode one stream of a fused GEMM item with its codeword index
+// (k_index_items): per segment of kIdxSegSyms symbols, lane l starts at the
+// recorded bit offset of symbol kIdxLaneSyms * l and decodes exactly
+// kIdxLaneSyms symbols into its slot of the symbol buffer, so the segment
+// needs no speculative prefix, no path resolution, no prefix sum and no
+// compaction.  The offsets are checked, not trusted: every lane must end
+// exactly where the next one starts (the last where the segment ends).  Lane
+// 0 of segment 0 starts at the stream's first bit, so by induction every
+// start is then a true codeword boundary and the symbols are exact.  When a
+// segment does not chain (a stale or damaged index, or a damaged stream),
+// it returns false with that segment's start in (rbit, rpos): the caller
+// continues the stream speculatively from there (decode_fast), which decodes
+// it -- or reports its error -- exactly as decode does.  Otherwise it returns
+// true with the stream's error bits in `err`.
+template <class Cons>
+__device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen,
+                                               const uint8_t* blk_end, Cons& C, const StreamIn& PN, bool next,
+                                               const uint16_t* idx, uint32_t& err, uint64_t& rbit, uint32_t& rpos) {
+  const uint64_t nbits = st.nbits;
+  const uint8_t* bend = st.bits + ((nbits + 7) >> 3);
+  if (bend > blk_end) bend = blk_end;
+  uint64_t segbit = 0;  // stream bit where the segment starts: a true codeword boundary
+  uint32_t pos0 = 0;
+  bool staged = false;
+  Fetch16 cur;
+  cur.v = make_uint4(0u, 0u, 0u, 0u);
+  cur.drop = 16;
+  for (uint32_t sg = 0; pos0 < st.count; ++sg) {
+    const uint16_t* e = idx + 64 * sg;
+    const uint32_t span = e[0];
+    const uint32_t rel = lane ? e[lane] : 0u;
+    const uint32_t rel_next = lane < 63 ? e[lane + 1] : span;
+    const uint32_t n_s = min(kIdxSegSyms, st.count - pos0);
+    const uint32_t last = (n_s - 1) / kIdxLaneSyms;  // last lane with symbols
+    const uint32_t k = lane < last ? kIdxLaneSyms : lane == last ? n_s - kIdxLaneSyms * last : 0u;
+    const uint32_t want = lane == last ? span : rel_next;
+    // Entries must lie inside the staged segment, in order, before any is used
+    // (lanes past the last one with symbols hold no entry).
+    if (__ballot(span > kIdxMaxSpan || (k && (rel > span || want < rel)))) {
+      rbit = segbit;
+      rpos = pos0;
+      return false;
+    }
+    if (sg) {  // this segment's bytes, prefetched during the previous one
+      stage_bits(S, lane, cur.value());
+      wave_sync();
+    }
+    const uint64_t nextbit = segbit + span;
+    const bool more = pos0 + n_s < st.count;
+    if (more && lane < kStreamLanes) cur = fetch16(st.bits + (nextbit >> 3) + 16 * lane, bend);
+    SmWin W;
+    issue_sm(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
+    // The staged buffer starts at byte segbit >> 3 (its bit 0 after the zero dword).
+    const uint32_t base = (uint32_t)(segbit & 7u), limit = base + want;
+    uint32_t p = base + rel, n = 0, d = 0, wi, w0, w1, w2;
+    load_window(S, p, wi, w0, w1, w2);
+    lds_bytes const o = as_lds(S.syms + kIdxLaneSyms * lane);
+    // A pair whose second symbol is not wanted (the lane's last symbol) stores
+    // it into the lane's own junk byte past the segment's symbols, so the
+    // step has no branch around the store.
+    lds_bytes const junk = as_lds(S.syms + kIdxSegSyms + lane);
+    // One exit condition: a lane walks exactly k symbols.  A path on wrong
+    // offsets (a stale index) advances at most 127 bits per step for at most
+    // kIdxLaneSyms steps, which stays inside this wave's LDS block, and fails
+    // the check below.
+    while (n < k) {
+      const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
+      uint32_t en = S.t.f.lut2[win >> (32 - kLutBits)];
+      if (en == kLongMark) {
+        const uint32_t lc = long_code(S, win, maxlen);
+        d |= lc == 0;
+        en = lc ? lc : kDeadMark;
+      }
+      const uint32_t pair = (en >> 15) & 1u, two = pair & (n + 1 < k ? 1u : 0u);
+      o[n] = (uint8_t)en;
+      (two ? o + n + 1 : junk)[0] = (uint8_t)(en >> 16);
+      p += pair & ~two ? (en >> 24) & 15u : (en >> 8) & 127u;
+      n += 1 + two;
+      slide(S, p, wi, w0, w1, w2);
+    }
+    if (__ballot(k && (d || p != limit))) {
+      rbit = segbit;
+      rpos = pos0;
+      return false;
+    }
+    wave_sync();
+    const bool fin = !more;
+    drain_loads();
+    if (fin && next) {
+      stage_inputs(S, lane, PN);
+      staged = true;
+    }
+    C.consume(S, lane, st, pos0, n_s, fin, W);
+    wave_sync();
+    pos0 += n_s;
+    segbit = nextbit;
+  }
+  // Every codeword is accounted for: the stream must end where its last one does.
+  if (next && !staged) {
+    drain_loads();
+    stage_inputs(S, lane, PN);
+  }
+  err = segbit == nbits ? 0u : (uint32_t)kErrStream;
+  return true;
+}
+
 // Bit-serial canonical decode for codes longer than 32 bits: lane 0 walks
 // the code one bit at a time (d = offset from the first code of the current
 // length); the consumer sees the symbols kSlowSeg at a time.
@@ -962,7 +1083,7 @@ __device__ __forceinline__ uint32_t fail_stream(Smem& S, uint32_t lane, uint32_t
 template <class Cons>
 __device__ __forceinline__ uint32_t stream_body(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end,
                                                 uint32_t count, uint32_t start, Cons& C, const NextStream& N,
-                                                StreamIn& PN) {
+                                                StreamIn& PN, const uint16_t* idx) {
   const uint64_t len = (uint64_t)(seg_end - seg);
   const uint64_t cnt = reinterpret_cast<const uint64_t*>(S.bcast)[0], nb = reinterpret_cast<const uint64_t*>(S.bcast)[1];
   const uint32_t lw = reinterpret_cast<const uint32_t*>(S.sorted)[lane];
@@ -978,20 +1099,24 @@ __device__ __forceinline__ uint32_t stream_body(Smem& S, uint32_t lane, const ui
   st.start = start;
   const Book b = build_book(S, lane, lw);
   if (b.err) return fail_stream(S, lane, b.err, N, PN);
-  const uint32_t err =
-      b.fast ? decode_fast(S, lane, st, b.maxlen, seg_end, C, PN, N.seg) : decode_slow(S, lane, st, C, PN, N.seg);
-  return err;
+  if (!b.fast) return decode_slow(S, lane, st, C, PN, N.seg);
+  uint64_t rbit = 0;
+  uint32_t rpos = 0, err = 0;
+  if (idx && idx[0] != kIdxNone && decode_indexed(S, lane, st, b.maxlen, seg_end, C, PN, N.seg, idx, err, rbit, rpos))
+    return err;
+  return decode_fast(S, lane, st, b.maxlen, seg_end, C, PN, N.seg, rbit, rpos);
 }
 
 // One stream whose inputs were staged in LDS (stage_inputs); the next
 // stream's inputs are issued into PN (when N.seg is given) early on, so they
 // load while this stream decodes, and staged when it finishes.  A stream that
-// fails before its last segment stages them on the way out.
+// fails before its last segment stages them on the way out.  `idx`: the
+// stream's codeword index (fused GEMM items), or nullptr.
 template <class Cons>
 __device__ __forceinline__ uint32_t run_stream(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end,
                                                uint32_t count, uint32_t start, Cons& C, const NextStream& N,
-                                               StreamIn& PN) {
-  return stream_body(S, lane, seg, seg_end, count, start, C, N, PN);
+                                               StreamIn& PN, const uint16_t* idx = nullptr) {
+  return stream_body(S, lane, seg, seg_end, count, start, C, N, PN, idx);
 }
 
 // ------------------------------------------------------------- consumers
@@ -1601,8 +1726,9 @@ k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_
     if (L.run) {
       Acc C(ga);
       C.init();
+      const uint16_t* idx = is.index ? is.index + (uint64_t)i * is.index_segs * 64 : nullptr;
       const uint32_t err = run_stream(S, lane, L.seg, L.end, L.count, L.s0, C,
-                                      NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN);
+                                      NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN, idx);
       float* slots = reinterpret_cast<float*>(S.syms);
       for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) slots[o] = 0.f;
       wave_sync();
@@ -1646,6 +1772,130 @@ __global__ void __launch_bounds__(64) k_gemm_finish(const DevBlock* __restrict__
       for (uint32_t k = 0; k < kMaxChunks; ++k) sum += v[k];
       Acc::store(ga, d.dst, o / Acc::kCols, o % Acc::kCols, sum);
     }
+  }
+}
+
+// ------------------------------------------------------ codeword index
+
+// 8 bytes at p as a big-endian (MSB-first) 64-bit value; bytes at or past
+// `end` read as zero.
+__device__ __forceinline__ uint64_t load_be64(const uint8_t* p, const uint8_t* end) {
+  uint64_t v;
+  if (p + 8 <= end) {
+    v = ldg64(p);
+  } else {
+    v = 0;
+    for (uint32_t i = 0; i < 8; ++i)
+      if (p + i < end) v |= (uint64_t)p[i] << (8 * i);
+  }
+  return __builtin_bswap64(v);
+}
+
+// Codeword index of the fused XKSP2 items (item i = substream i % kMaxChunks
+// of block i / kMaxChunks), the load-time sidecar of static weights.  One lane
+// per item: the lane checks its block and substream headers as decode does,
+// builds the canonical per-length limits of its code lengths in its own LDS
+// slice (lim[l] = left-aligned end of the codes of length <= l, the closed
+// form of build_fast), and walks the code once, recording the bit offset of
+// every kIdxLaneSyms-th codeword and each segment's length.  An item whose
+// stream is invalid, has codes longer than 32 bits, or has a segment longer
+// than kIdxMaxSpan bits gets kIdxNone: the fused kernels decode it
+// speculatively and report its errors exactly as decode does.
+struct IdxLane {
+  uint64_t lim[34];
+};
+__global__ void __launch_bounds__(64) k_index_items(const DevBlock* __restrict__ blocks, uint32_t nblocks,
+                                                    const uint8_t* __restrict__ arc, uint16_t* __restrict__ index,
+                                                    uint32_t segs) {
+  __shared__ IdxLane Lanes[64];
+  uint64_t* lim = Lanes[threadIdx.x].lim;
+  const uint32_t nitems = nblocks * kMaxChunks;
+  for (uint32_t i = blockIdx.x * 64 + threadIdx.x; i < nitems; i += gridDim.x * 64) {
+    uint16_t* out = index + (uint64_t)i * segs * 64;
+    const DevBlock d = blocks[i / kMaxChunks];
+    const uint32_t k = i % kMaxChunks;
+    const uint8_t* blk = arc + d.src;
+    bool ok = false;
+    if (d.size >= 32) {
+      const uint64_t magic = ldg64(blk), rows = ldg64(blk + 8), cols = ldg64(blk + 16), chunks = ldg64(blk + 24);
+      const bool head = magic == kMagicXKSP2 && rows == d.rows && cols == d.cols && rows && rows <= 16 && cols &&
+                        cols <= kMaxBlockElems / rows && chunks && chunks <= kMaxChunks &&
+                        chunks <= rows * cols && d.size >= 32 + 8 * chunks && k < chunks;
+      uint64_t off = 32 + 8 * chunks, len = 0;
+      bool seg_ok = head;
+      for (uint32_t q = 0; seg_ok && q <= k; ++q) {
+        len = ldg64(blk + 32 + 8 * q);
+        if (len < 272 || len > d.size - off) seg_ok = false;
+        else if (q < k) off += len;
+      }
+      const uint64_t total = rows * cols;
+      const uint64_t s0 = seg_ok ? total * k / chunks : 0, count = seg_ok ? total * (k + 1) / chunks - s0 : 0;
+      const uint8_t* seg = blk + off;
+      uint64_t cnt = 0, nb = 0;
+      if (seg_ok) {
+        cnt = ldg64(seg);
+        nb = ldg64(seg + 8);
+        seg_ok = cnt == count && cnt <= len - 272 && nb / 8 + (nb % 8 != 0) == len - 272 - cnt &&
+                 count <= (uint64_t)segs * kIdxSegSyms && count > 0;
+      }
+      uint32_t minlen = 64, maxlen = 0;
+      if (seg_ok) {
+        for (uint32_t l = 0; l < 34; ++l) lim[l] = 0;
+        for (uint32_t q = 0; q < 64; ++q) {
+          const uint32_t w = ldg32(seg + 16 + 4 * q);
+          for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t l = (w >> (8 * j)) & 255u;
+            if (l > kMaxLenFast) seg_ok = false;
+            else if (l) {
+              lim[l] += 1;
+              minlen = min(minlen, l);
+              maxlen = max(maxlen, l);
+            }
+          }
+        }
+        uint64_t acc = 0;
+        for (uint32_t l = 1; seg_ok && l <= kMaxLenFast; ++l) {
+          acc += lim[l] << (32 - l);
+          lim[l] = acc;
+        }
+        if (acc > (1ull << 32) || !maxlen) seg_ok = false;
+      }
+      if (seg_ok) {
+        const uint8_t* bits = seg + 272 + cnt;
+        const uint8_t* bend = bits + (nb + 7) / 8;
+        uint64_t p = 0, segstart = 0, cb = 0, cur = load_be64(bits, bend);
+        bool walk = true;
+        for (uint64_t n = 0; walk && n < count; ++n) {
+          if (n % kIdxLaneSyms == 0) {
+            const uint64_t sgi = n / kIdxSegSyms, ln = (n / kIdxLaneSyms) % 64;
+            if (ln == 0) {
+              if (n) {
+                if (p - segstart > kIdxMaxSpan) walk = false;
+                out[(sgi - 1) * 64] = (uint16_t)(p - segstart);
+              }
+              segstart = p;
+            } else {
+              out[sgi * 64 + ln] = (uint16_t)(p - segstart);
+            }
+          }
+          if (p + 32 > 8 * cb + 64) {
+            cb = p >> 3;
+            cur = load_be64(bits + cb, bend);
+          }
+          const uint64_t w = (cur << (p - 8 * cb)) >> 32;
+          uint32_t l = minlen;
+          while (l <= maxlen && w >= lim[l]) ++l;
+          if (l > maxlen) walk = false;
+          p += l;
+          if (p > nb) walk = false;
+        }
+        if (walk && p == nb && p - segstart <= kIdxMaxSpan) {
+          out[((count - 1) / kIdxSegSyms) * 64] = (uint16_t)(p - segstart);
+          ok = true;
+        }
+      }
+    }
+    if (!ok) out[0] = kIdxNone;
   }
 }
 
@@ -1904,6 +2154,16 @@ hipError_t launch_or_status(const uint32_t* status, uint32_t n, uint32_t* flags,
   if (!n) return hipSuccess;
   const unsigned g = (n + 255) / 256;
   hipLaunchKernelGGL(k_or_status, dim3(g < 64 ? g : 64u), dim3(256), 0, s, status, n, flags);
+  return hipGetLastError();
+}
+
+hipError_t launch_index_items(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint16_t* index,
+                              uint32_t segs, hipStream_t s) {
+  if (!nblocks) return hipSuccess;
+  const uint64_t items = (uint64_t)nblocks * kMaxChunks;
+  const uint64_t g = (items + 63) / 64;
+  hipLaunchKernelGGL(k_index_items, dim3(g < 4096 ? (unsigned)g : 4096u), dim3(64), 0, s, blocks, nblocks, arc, index,
+                     segs);
   return hipGetLastError();
 }
 

@@ -46,9 +46,20 @@ constexpr uint32_t kMaxFusedBatch = 16;
 // partial-sum slots of kMaxItemOut floats and the block's substream count
 // (written by the item kernel; 0 = header error).
 constexpr uint32_t kMaxItemOut = 16 * kMaxFusedBatch;
+// Codeword index of the fused XKSP2 items (a load-time sidecar of static
+// weights): per item, `index_segs` segments of kIdxSegSyms symbols, each 64
+// u16 entries: entry 0 = the segment's length in code bits, entry l (l >= 1)
+// = the bit offset of symbol kIdxLaneSyms * l from the segment's start.
+// Entry 0 of segment 0 holds kIdxNone when the item has no index (its stream
+// does not fit the indexed path); the kernels then decode it speculatively.
+constexpr uint32_t kIdxLaneSyms = 32;
+constexpr uint32_t kIdxSegSyms = 64 * kIdxLaneSyms;
+constexpr uint16_t kIdxNone = 0xFFFF;
 struct ItemScratch {
-  float* partial;  // [blocks][kMaxChunks][kMaxItemOut]
-  uint32_t* done;  // [blocks]
+  float* partial;         // [blocks][kMaxChunks][kMaxItemOut]
+  uint32_t* done;         // [blocks]
+  const uint16_t* index;  // [items][index_segs][64], or nullptr
+  uint32_t index_segs;
 };
 constexpr uint64_t kItemScratchPerBlock = (uint64_t)kMaxChunks * kMaxItemOut * 4 + 4;
 
