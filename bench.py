@@ -118,6 +118,22 @@ def time_events(torch, fn, steps: int, stream) -> float:
     return start.elapsed_time(end) / steps
 
 
+def time_samples(torch, fn, samples: int, per_sample: int, stream) -> dict:
+    """Per-call milliseconds of fn(): `samples` samples of `per_sample` back-to-back calls,
+    each bracketed by HIP events on `stream`; median with p10 / p90."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(samples)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        a.record(stream)
+        for _ in range(per_sample):
+            fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = np.array([a.elapsed_time(b) / per_sample for a, b in evs])
+    return {"median": float(np.median(ms)), "p10": float(np.percentile(ms, 10)), "p90": float(np.percentile(ms, 90)),
+            "mean": float(ms.mean()), "samples": samples, "calls_per_sample": per_sample}
+
+
 def gemv_bench(torch, lib, rows: int, cols: int, copies: int, steps: int, warmup: int, stream) -> dict:
     """Fused batch-1 decode-GEMV over `copies` resident copies of one parallel32 layer."""
     import xksv_hip
@@ -137,18 +153,32 @@ def gemv_bench(torch, lib, rows: int, cols: int, copies: int, steps: int, warmup
         plan.gemm(arcs[it[0] % copies].data_ptr(), x.data_ptr(), 1, y.data_ptr(), s)
         it[0] += 1
 
+    # The first GEMM call on a plan prepares it: block routing and the codeword index of the
+    # static weights (one lane per substream, k_index_items); timed on its own.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    prep_ms = (time.perf_counter() - t0) * 1e3
     for _ in range(max(warmup, 1) * copies):
         step()
     nbad = plan.errors(s)[0]
     ref = (w.double() @ x.double())
     rel = (torch.linalg.norm(y.double() - ref) / torch.linalg.norm(ref)).item()
-    ms = time_events(torch, step, steps * copies, stream)
+    t = time_samples(torch, step, max(steps, 20), copies, stream)
+    ms = t["median"]
     plan.close()
-    alg = enc.nbytes + cols * 4 + rows * 4
-    return {"us_per_layer": round(ms * 1e3, 2), "encoded_bytes": int(enc.nbytes),
+    # Index: per substream, ceil(symbols / 2048) segments of 64 u16 offsets (read once per call).
+    nsub = int((table["codec"] == 2).sum()) * 32
+    segs = max(1, -(-(16 * cols // 32) // 2048))
+    index_bytes = nsub * segs * 128
+    alg = enc.nbytes + index_bytes + cols * 4 + rows * 4
+    return {"us_per_layer": round(ms * 1e3, 2), "us_p10": round(t["p10"] * 1e3, 2), "us_p90": round(t["p90"] * 1e3, 2),
+            "encoded_bytes": int(enc.nbytes), "index_bytes": index_bytes, "index_build_ms": round(prep_ms, 3),
             "algorithmic_bytes": int(alg), "gbps": round(alg / (ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "rel_l2_vs_fp64": rel,
-            "errors": int(nbad), "copies": copies}
+            "errors": int(nbad), "copies": copies, "timing": "median of %d samples of %d rotating calls" % (
+                t["samples"], copies)}
 
 
 def gemm_bf16_bench(torch, lib, rows: int, cols: int, batches, copies: int, steps: int, warmup: int, stream) -> dict:
@@ -178,9 +208,13 @@ def gemm_bf16_bench(torch, lib, rows: int, cols: int, batches, copies: int, step
         nbad = plan.errors(s)[0]
         ref = x.double() @ w.double().T
         rel = (torch.linalg.norm(y.double() - ref) / torch.linalg.norm(ref)).item()
-        ms = time_events(torch, step, steps * copies, stream)
-        alg = enc.nbytes + batch * cols * 2 + batch * rows * 4
-        out[str(batch)] = {"us_per_layer": round(ms * 1e3, 2), "gbps": round(alg / (ms * 1e-3) / 1e9, 1),
+        t = time_samples(torch, step, max(steps, 20), copies, stream)
+        ms = t["median"]
+        nsub = int((table["codec"] == 2).sum()) * 32
+        index_bytes = nsub * max(1, -(-(16 * cols // 32) // 2048)) * 128
+        alg = enc.nbytes + index_bytes + batch * cols * 2 + batch * rows * 4
+        out[str(batch)] = {"us_per_layer": round(ms * 1e3, 2), "us_p10": round(t["p10"] * 1e3, 2),
+                           "us_p90": round(t["p90"] * 1e3, 2), "gbps": round(alg / (ms * 1e-3) / 1e9, 1),
                            "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "rel_l2_vs_fp64": rel,
                            "mfma": batch >= 8, "errors": int(nbad)}
         del ref
@@ -188,9 +222,11 @@ def gemm_bf16_bench(torch, lib, rows: int, cols: int, batches, copies: int, step
     return {"encoded_bytes": int(enc.nbytes), "copies": copies, "batches": out}
 
 
-def small_archive_bench(torch, lib, tensors, codec: int, steps: int, warmup: int, stream) -> dict:
-    """Decode GB/s of a small archive (repeated steps; it fits in the last-level cache, so this is
-    a parity-and-throughput report, not a roofline figure) plus a bit-exact check."""
+def small_archive_bench(torch, lib, tensors, codec: int, steps: int, warmup: int, stream, copies: int = 1) -> dict:
+    """Decode GB/s of a small archive plus a bit-exact check.  With copies > 1 the steps rotate
+    over that many resident copies of the archive and of the output (a working set beyond the
+    256 MB last-level cache), so the figure is an HBM roofline figure; with one copy the archive
+    stays in the cache and the figure is a throughput report only."""
     import xksv_hip
     encs, tables, words_all = [], [], []
     arc_off = out_off = 0
@@ -229,10 +265,27 @@ def small_archive_bench(torch, lib, tensors, codec: int, steps: int, warmup: int
     nbad = plan.errors(s)[0]
     want = torch.from_numpy(np.concatenate(words_all).view(np.uint8)).to("cuda")
     exact = nbad == 0 and torch.equal(d_out, want)
-    ms = time_events(torch, lambda: plan.decode(d_arc.data_ptr(), d_out.data_ptr(), out_off, s), steps, stream)
+    arcs = [d_arc] + [d_arc.clone() for _ in range(copies - 1)]
+    outs = [d_out] + [torch.empty_like(d_out) for _ in range(copies - 1)]
+    it = [0]
+
+    def step():
+        k = it[0] % copies
+        plan.decode(arcs[k].data_ptr(), outs[k].data_ptr(), out_off, s)
+        it[0] += 1
+
+    t = time_samples(torch, step, max(steps, 10), copies, stream)
+    ms = t["median"]
+    exact = exact and plan.errors(s)[0] == 0 and all(torch.equal(o, want) for o in outs[1:])
     plan.close()
-    return {"blocks": int(len(table)), "encoded_bytes": int(d_arc.numel()), "decoded_bytes": int(out_off),
-            "ms": round(ms, 4), "decoded_gbps": round(out_off / (ms * 1e-3) / 1e9, 1), "bit_exact": bool(exact)}
+    alg = int(d_arc.numel()) + out_off
+    r = {"blocks": int(len(table)), "encoded_bytes": int(d_arc.numel()), "decoded_bytes": int(out_off),
+         "ms": round(ms, 4), "ms_p10": round(t["p10"], 4), "ms_p90": round(t["p90"], 4),
+         "decoded_gbps": round(out_off / (ms * 1e-3) / 1e9, 1), "bit_exact": bool(exact), "copies": copies}
+    if copies > 1:
+        r["working_set_bytes"] = alg * copies
+        r["roofline_frac"] = round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    return r
 
 
 def copy_bench(torch, steps: int, stream) -> float:
@@ -256,7 +309,11 @@ def cpu_baseline(encs, table, max_slabs: int) -> dict | None:
     step = 1 if max_slabs <= 0 else max(1, -(-len(comp) // max_slabs))
     sample = comp[::step]
     raw = int(sample["raw_size"].sum())
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    # All the cores this job is allotted: the affinity mask, capped by the CPU share the
+    # host grants a one-GPU job (OMP_NUM_THREADS, which it sets), whatever nproc shows.
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", affinity) or affinity)
+    cores = max(1, min(affinity, share))
 
     def one(t):
         i = int(np.searchsorted(bases, t["offset"], side="right")) - 1
@@ -271,8 +328,51 @@ def cpu_baseline(encs, table, max_slabs: int) -> dict | None:
     if any(rcs):
         return None
     return {"value": round(raw / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
+            "nproc": os.cpu_count(), "affinity_cpus": affinity, "cpu_share": share, "cpu_model": cpu_model(),
             "sample": (f"{'every' if step == 1 else f'every {step}th'} parallel32 block of the archive "
-                       f"({len(sample)} blocks, {raw / 1e9:.2f} GB decoded), {dt:.1f}s wall on {cores} threads")}
+                       f"({len(sample)} blocks, {raw / 1e9:.2f} GB decoded), {dt:.1f}s wall on {cores} threads "
+                       f"(the job's CPU share)")}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def abi_bench(torch, lib, warmup: int = 2, repeats: int = 10) -> dict:
+    """The reference's per-block methodology (python/bench_parallel_decode.py:22-38): the
+    host-pointer drop-in entry xksv_hip_decode_parallel / xksv_hip_decode on one block whose
+    bytes are in host memory -- staging copy, launch and synchronisation included -- 2 warm-ups,
+    median of 10, for the 16x4096 and 16x256 blocks of docs/benchmark-parallel-decode.json."""
+    import xksv_synth as syn
+    out = {}
+    for rows, cols in ((16, 4096), (16, 256)):
+        w = syn.normal_bf16(0, (rows, cols))
+        raw = w.astype("<u2").tobytes()
+        d = torch.empty(len(raw), dtype=torch.uint8, device="cuda")
+        r = {}
+        for name, op, call in (("parallel32", "xksv_pack_parallel", lambda b: lib.decode_parallel(b, d.data_ptr())),
+                               ("serial", "xksv_pack", lambda b: lib.decode(b, rows, cols, d.data_ptr()))):
+            blob = lib.call(op, raw, rows, cols)
+            for _ in range(warmup):
+                assert call(blob) == 0
+            ts = []
+            for _ in range(repeats):
+                t0 = time.perf_counter()
+                rc = call(blob)
+                ts.append((time.perf_counter() - t0) * 1e3)
+                assert rc == 0
+            ok = d.cpu().numpy().tobytes() == raw
+            r[name] = {"ms_median": round(float(np.median(ts)), 4), "encoded_bytes": len(blob), "bit_exact": ok}
+        out[f"{rows}x{cols}"] = r
+    out["reference_rtx3090ti_ms"] = {"16x4096": {"serial": 24.63, "parallel32": 2.446},
+                                     "16x256": {"serial": 1.647, "parallel32": 0.2907}}
+    return out
 
 
 def digest_bench(torch, plan, d_out, raw_total, table, steps, stream):
@@ -348,7 +448,8 @@ def main() -> int:
     nbad, first, bits = plan.errors(s)
     verified = nbad == 0 and verify(torch, d_out, meta)
     log(f"decode errors={nbad} verified={verified}")
-    ms = time_events(torch, step, args.steps, stream)
+    tdec = time_samples(torch, step, args.steps, 1, stream)
+    ms = tdec["median"]
     nbad2 = plan.errors(s)[0]
     decoded_gbps = raw_total / (ms * 1e-3) / 1e9
     # Dominant kernel: the parallel32 decode launch.  Its algorithmic bytes are the encoded
@@ -371,7 +472,7 @@ def main() -> int:
                                       stream) for r, c in ((28672, 8192), (8192, 28672))}
     log("gemm bf16 " + "; ".join(f"{k}: " + ", ".join(f"b{b} {v['us_per_layer']} us" for b, v in g["batches"].items())
                                  for k, g in g5.items()))
-    c1 = small_archive_bench(torch, lib, [((4096, 4096), "normal", 0)], 1, args.steps, args.warmup, stream)
+    c1 = small_archive_bench(torch, lib, [((4096, 4096), "normal", 0)], 1, args.steps, args.warmup, stream, copies=20)
     mixed = [((4096, 4096), "normal", 1), ((4096, 4096), "student_t", 2), ((4096, 4096), "uniform", 3),
              ((4096, 4096), "zeros", 4), ((4096,), "fp32", 5)]
     c3 = {"serial": small_archive_bench(torch, lib, mixed, 1, args.steps, args.warmup, stream),
@@ -379,6 +480,9 @@ def main() -> int:
     log(f"4096x4096 serial {c1['decoded_gbps']} GB/s exact={c1['bit_exact']}; mixed serial "
         f"{c3['serial']['decoded_gbps']} / parallel {c3['parallel']['decoded_gbps']} GB/s")
     copy_gbps = copy_bench(torch, 10, stream)
+    abi = abi_bench(torch, lib)
+    log("host-pointer ABI per block: " + ", ".join(f"{k} {v['parallel32']['ms_median']} / {v['serial']['ms_median']} ms"
+                                                   for k, v in abi.items() if isinstance(v, dict) and "serial" in v))
 
     traffic = None
     tpath = ROOT / "profiles" / "decode_llama3_8b_traffic.json"
@@ -402,6 +506,8 @@ def main() -> int:
                      "kernel": "k_decode_parallel", "algorithmic_bytes_per_launch": alg_bytes},
         "cpu_baseline": cpu,
         "bit_exact_full_size": bool(verified and nbad2 == 0),
+        "decode_ms": {k: round(v, 4) for k, v in tdec.items() if k in ("median", "p10", "p90", "mean")},
+        "host_pointer_abi": abi,
         "hbm_pct_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "gemv_us_per_layer_14336x4096": g1["us_per_layer"],
         "gemv_14336x4096": g1, "gemv_4096x14336": g2,
