@@ -1288,8 +1288,10 @@ struct GemmF32 {
 };
 
 // bf16 activations in the layout of x @ W.T: X[j * ldx + c] (batch rows),
-// Y[j * ldy + dst + r]; VALU FMAs in fp32 (batch < 8).  Same lane mapping as
-// GemmF32.
+// Y[j * ldy + dst + r]; fp32 accumulation on the VALU (batch < 8).  A decoded
+// unit is already 8 bf16 weights in 4 packed pairs, and 8 columns of an X row
+// are 4 pairs too, so each pair of products is one v_dot2c_f32_bf16 (the
+// products of bf16 values are exact in fp32).  Same lane mapping as GemmF32.
 template <int NB>
 struct GemmBf16 {
   static constexpr int kCols = NB, kOut = 16 * NB;
@@ -1310,28 +1312,29 @@ struct GemmBf16 {
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = 0.f;
   }
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    bf16x2 va, vb;
+    __builtin_memcpy(&va, &a, 4);
+    __builtin_memcpy(&vb, &b, 4);
+    return __builtin_amdgcn_fdot2_f32_bf16(va, vb, c, false);
+  }
   __device__ __forceinline__ void unit(const Smem& S, const Stream& st, uint32_t pos0, uint32_t u, uint64_t M) {
     uint64_t E;
     __builtin_memcpy(&E, S.syms + 8 * u, 8);
     const uint4 w = combine8(E, M);
     const uint32_t U = ((st.start + pos0) >> 3) + u;
     const uint64_t col = 16ull * (U >> 5) + 8u * (U & 1u);
-    const float f[8] = {bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y),
-                        bf_lo(w.z), bf_hi(w.z), bf_lo(w.w), bf_hi(w.w)};
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       if (j < (int)nb) {
         uint4 xv;
         __builtin_memcpy(&xv, x + j * ldx + col, 16);
         float a = acc[j];
-        a = fmaf(f[0], bf_lo(xv.x), a);
-        a = fmaf(f[1], bf_hi(xv.x), a);
-        a = fmaf(f[2], bf_lo(xv.y), a);
-        a = fmaf(f[3], bf_hi(xv.y), a);
-        a = fmaf(f[4], bf_lo(xv.z), a);
-        a = fmaf(f[5], bf_hi(xv.z), a);
-        a = fmaf(f[6], bf_lo(xv.w), a);
-        a = fmaf(f[7], bf_hi(xv.w), a);
+        a = dot2(w.x, xv.x, a);
+        a = dot2(w.y, xv.y, a);
+        a = dot2(w.z, xv.z, a);
+        a = dot2(w.w, xv.w, a);
         acc[j] = a;
       }
     }
