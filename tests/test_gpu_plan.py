@@ -197,7 +197,7 @@ def _resplit(hip, oracle, w, chunks) -> bytes:
 def test_plan_gemm_nonstandard_chunk_counts(hip, oracle, batch):
     """Plan GEMMs over XKSP2 blocks re-split into 32, 5, 7, 1, 31 and 16 substreams: blocks
     whose substreams do not start on 8-element boundaries are routed to decode + plain GEMM,
-    the others to the fused kernels; fp32 X and bf16 X (MFMA from batch 8) both match fp64."""
+    the others to the fused kernels; fp32 X and bf16 X (MFMA from batch 2) both match fp64."""
     cols = 1024
     counts = (32, 5, 7, 1, 31, 16)
     w = syn.normal_bf16(900 + batch, (16 * len(counts), cols))
@@ -224,6 +224,50 @@ def test_plan_gemm_nonstandard_chunk_counts(hip, oracle, batch):
         assert plan.errors()[0] == 0
         want = (xb.double() @ wt.T).cpu().numpy()
         assert np.linalg.norm(yb.cpu().numpy() - want) / np.linalg.norm(want) <= 2e-3
+    finally:
+        plan.close()
+
+
+@pytest.mark.parametrize("cols", [4096, 4112])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 16])
+def test_plan_gemm_staged_x(hip, batch, cols):
+    """Indexed fused GEMMs copy each segment's x columns into LDS when x and its rows are
+    16-byte aligned, and read x from global memory otherwise (x shifted by one element).
+    4096 columns: substreams of whole tiles (bf16 MFMA from batch 2, 8-tile segments);
+    4112: substreams start mid-tile (VALU consumers, 9-tile segments).  Both layouts, both
+    activation types, both placements match fp64; runs at one placement are bit-identical
+    to each other."""
+    rows = 64
+    w = syn.normal_bf16(1300 + cols + batch, (rows, cols))
+    enc, table = hip.encode_tensor(w, 2)
+    table = table.copy()
+    table["out_offset"] //= cols * 2
+    d_arc = _upload(enc)
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    wt = torch.from_numpy(syn.bf16_to_f32(w).astype(np.float64)).to("cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(batch)
+    try:
+        for shift in (0, 1):
+            xbuf = torch.randn(batch * cols + 8, generator=g, device="cuda")
+            xb = xbuf.to(torch.bfloat16)[shift:shift + batch * cols].view(batch, cols)
+            assert (xb.data_ptr() % 16 == 0) == (shift == 0)
+            yb = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
+            plan.gemm_bf16(d_arc.data_ptr(), xb.data_ptr(), batch, yb.data_ptr())
+            assert plan.errors()[0] == 0
+            want = (xb.double() @ wt.T).cpu().numpy()
+            err = np.linalg.norm(yb.cpu().numpy() - want) / np.linalg.norm(want)
+            assert err <= 2e-3 and err <= 1e-5, (shift, err)
+            yb2 = torch.empty_like(yb)
+            plan.gemm_bf16(d_arc.data_ptr(), xb.data_ptr(), batch, yb2.data_ptr())
+            assert torch.equal(yb, yb2)
+            xf = xbuf[shift:shift + batch * cols].view(cols, batch)
+            yf = torch.full((rows, batch), float("nan"), dtype=torch.float32, device="cuda")
+            plan.gemm(d_arc.data_ptr(), xf.data_ptr(), batch, yf.data_ptr())
+            assert plan.errors()[0] == 0
+            want = (wt @ xf.double()).cpu().numpy()
+            err = np.linalg.norm(yf.cpu().numpy() - want) / np.linalg.norm(want)
+            assert err <= 1e-5, (shift, err)
     finally:
         plan.close()
 

@@ -103,6 +103,11 @@ struct alignas(16) Smem {
   uint32_t bcast[4];
   alignas(16) uint8_t syms[kSymsBytes];
 };
+// X columns of one indexed segment, staged for the fused GEMM consumers: in
+// the symbol buffer past the segment's symbols and the lanes' junk bytes.
+constexpr uint32_t kXOff = kIdxSegSyms + 256;
+constexpr uint32_t kXBytes = 4096;
+static_assert(kXOff + kXBytes <= kSymsBytes, "staged X must fit the symbol buffer");
 
 // ------------------------------------------------------------------ helpers
 
@@ -687,6 +692,21 @@ struct NextStream {
 // consumer's fresh stores.
 __device__ __forceinline__ void drain_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0) only
 
+// 16 bytes from global memory straight into LDS (global_load_lds_dwordx4):
+// lane l writes the 16 bytes at its `src` to dst + 16 l.  `dst` is the same
+// on every lane and 16-byte aligned; every lane's src must be readable.  The
+// copy is an outstanding load until drain_loads().
+__device__ __forceinline__ void copy_to_lds16(const void* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+// 16 bytes of LDS through an LDS pointer: a read that the compiler could
+// otherwise merge with a global read of the other branch into one FLAT load.
+__device__ __forceinline__ uint4 lds16(const uint8_t* p) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = *(__attribute__((address_space(3))) const u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ void stage_bits(Smem& S, uint32_t lane, uint4 v) {
   if (lane < kStreamLanes) {
     uint32_t* w = &S.stream[1 + 4 * lane];
@@ -940,6 +960,7 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
     // Entries must lie inside the staged segment, in order, before any is used
     // (lanes past the last one with symbols hold no entry).
     if (__ballot(span > kIdxMaxSpan || (k && (rel > span || want < rel)))) {
+      C.xs = false;  // the previous segment's copy has landed (drained before its consume)
       rbit = segbit;
       rpos = pos0;
       return false;
@@ -953,6 +974,7 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
     if (more && lane < kStreamLanes) cur = fetch16(st.bits + (nextbit >> 3) + 16 * lane, bend);
     SmWin W;
     issue_sm(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
+    C.stage_x(S, lane, st, pos0, n_s);  // lands in LDS during the walk
     // The staged buffer starts at byte segbit >> 3 (its bit 0 after the zero dword).
     const uint32_t base = (uint32_t)(segbit & 7u), limit = base + want;
     uint32_t p = base + rel, n = 0, d = 0, wi, w0, w1, w2;
@@ -982,6 +1004,8 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
       slide(S, p, wi, w0, w1, w2);
     }
     if (__ballot(k && (d || p != limit))) {
+      drain_loads();  // the X copy must land before decode_fast reuses the buffer
+      C.xs = false;
       rbit = segbit;
       rpos = pos0;
       return false;
@@ -1135,6 +1159,8 @@ struct Writer {
   uint64_t rows, cols;
   uint32_t tpb;  // tiles per 16-row band
   bool aligned;
+  bool xs = false;  // no activations
+  __device__ __forceinline__ void stage_x(Smem&, uint32_t, const Stream&, uint32_t, uint32_t) {}
   static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) { return lane; }
   __device__ __forceinline__ void unit(const Smem& S, const Stream& st, uint32_t pos0, uint32_t u, uint64_t M) const {
     uint64_t E;
@@ -1209,9 +1235,19 @@ struct GemmF32 {
   const float* x;
   uint64_t ldx;
   uint32_t nb;
+  bool xa;          // x is 16-byte aligned
+  bool xs = false;  // this segment's x columns are staged in LDS (kXOff)
   float acc[NB];
   __device__ __forceinline__ explicit GemmF32(const GemmArgs& a)
-      : x(static_cast<const float*>(a.x)), ldx(a.ldx), nb(a.nb) {}
+      : x(static_cast<const float*>(a.x)), ldx(a.ldx), nb(a.nb), xa(((uintptr_t)a.x & 15u) == 0) {}
+  // One-column x (NB == 1): the segment's tiles t .. t + 8 need x[16 t, 16 t
+  // + 144), at most 36 pieces of 16 bytes, one LDS copy.
+  __device__ __forceinline__ void stage_x(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t n) {
+    xs = NB == 1 && xa;
+    if (!xs) return;
+    const uint32_t a = st.start + pos0, t = a >> 8, tiles = ((a + n - 1) >> 8) - t + 1;
+    copy_to_lds16(lane < 4 * tiles ? x + 16ull * t + 4 * lane : x, S.syms + kXOff);
+  }
   static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) { return lane; }
   static __device__ __forceinline__ bool fits(uint32_t s0, uint32_t count, uint64_t rows, uint64_t cols) {
     return unit_aligned(s0, count, rows, cols);
@@ -1233,8 +1269,15 @@ struct GemmF32 {
                         bf_lo(w.z), bf_hi(w.z), bf_lo(w.w), bf_hi(w.w)};
     if (NB == 1) {
       float4 xa, xb;
-      __builtin_memcpy(&xa, x + col, 16);
-      __builtin_memcpy(&xb, x + col + 4, 16);
+      if (xs) {
+        const uint32_t o = kXOff + 4u * (uint32_t)(col - 16ull * ((st.start + pos0) >> 8));
+        const uint4 va = lds16(S.syms + o), vb = lds16(S.syms + o + 16);
+        __builtin_memcpy(&xa, &va, 16);
+        __builtin_memcpy(&xb, &vb, 16);
+      } else {
+        __builtin_memcpy(&xa, x + col, 16);
+        __builtin_memcpy(&xb, x + col + 4, 16);
+      }
       float a = acc[0];
       a = fmaf(f[0], xa.x, a);
       a = fmaf(f[1], xa.y, a);
@@ -1288,19 +1331,37 @@ struct GemmF32 {
 };
 
 // bf16 activations in the layout of x @ W.T: X[j * ldx + c] (batch rows),
-// Y[j * ldy + dst + r]; fp32 accumulation on the VALU (batch < 8).  A decoded
+// Y[j * ldy + dst + r]; fp32 accumulation on the VALU (batch 1, or streams
+// that do not cover whole tiles).  A decoded
 // unit is already 8 bf16 weights in 4 packed pairs, and 8 columns of an X row
 // are 4 pairs too, so each pair of products is one v_dot2c_f32_bf16 (the
 // products of bf16 values are exact in fp32).  Same lane mapping as GemmF32.
 template <int NB>
 struct GemmBf16 {
   static constexpr int kCols = NB, kOut = 16 * NB;
+  static constexpr uint32_t kXRow = 18;  // staged 16-byte pieces per x row: 9 tiles
+  static constexpr uint32_t kXCopies = NB <= 8 ? (kXRow * NB + 63) / 64 : 0;
   const uint16_t* x;
   uint64_t ldx;
   uint32_t nb;
+  bool xa;          // x and its row stride are 16-byte aligned
+  bool xs = false;  // this segment's x columns are staged in LDS (kXOff)
   float acc[NB];
   __device__ __forceinline__ explicit GemmBf16(const GemmArgs& a)
-      : x(static_cast<const uint16_t*>(a.x)), ldx(a.ldx), nb(a.nb) {}
+      : x(static_cast<const uint16_t*>(a.x)), ldx(a.ldx), nb(a.nb),
+        xa(((uintptr_t)a.x & 15u) == 0 && a.ldx % 8 == 0) {}
+  // Rows j < nb of the segment's columns [16 t, 16 t + 144): piece q of the
+  // copies is row q / kXRow, columns 8 (q % kXRow) on.
+  __device__ __forceinline__ void stage_x(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t n) {
+    xs = kXCopies && xa;
+    if (!xs) return;
+    const uint32_t a = st.start + pos0, t = a >> 8, tiles = ((a + n - 1) >> 8) - t + 1;
+#pragma unroll
+    for (uint32_t i = 0; i < kXCopies; ++i) {
+      const uint32_t q = kWave * i + lane, j = q / kXRow, pc = q - kXRow * j;
+      copy_to_lds16(j < nb && pc < 2 * tiles ? x + j * ldx + 16ull * t + 8 * pc : x, S.syms + kXOff + 1024 * i);
+    }
+  }
   static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) { return lane; }
   static __device__ __forceinline__ bool fits(uint32_t s0, uint32_t count, uint64_t rows, uint64_t cols) {
     return unit_aligned(s0, count, rows, cols);
@@ -1329,7 +1390,10 @@ struct GemmBf16 {
     for (int j = 0; j < NB; ++j) {
       if (j < (int)nb) {
         uint4 xv;
-        __builtin_memcpy(&xv, x + j * ldx + col, 16);
+        if (xs)
+          xv = lds16(S.syms + kXOff + 16u * (kXRow * j + (uint32_t)(col / 8 - 2ull * ((st.start + pos0) >> 8))));
+        else
+          __builtin_memcpy(&xv, x + j * ldx + col, 16);
         float a = acc[j];
         a = dot2(w.x, xv.x, a);
         a = dot2(w.y, xv.y, a);
@@ -1368,7 +1432,7 @@ struct GemmBf16 {
 };
 
 // bf16 activations (layout of GemmBf16), bf16 MFMA with fp32 accumulation
-// (batch 8..16, padded to 16): v_mfma_f32_16x16x32_bf16 multiplies a 16 x 32
+// (batch 2..16, padded to 16): v_mfma_f32_16x16x32_bf16 multiplies a 16 x 32
 // slice of W (two 16x16 tiles side by side) by a 32 x 16 slice of X.  Lane
 // l = r + 16 g supplies W row r, columns 8g..8g+7 of the slice -- exactly one
 // decoded unit (half a tile row, unit 32 (g / 2) + 2 r + g % 2 of the tile
@@ -1382,9 +1446,24 @@ struct GemmMfma {
   const uint16_t* x;
   uint64_t ldx;
   uint32_t nb;
+  bool xa;          // x and its row stride are 16-byte aligned
+  bool xs = false;  // this segment's x columns are staged in LDS (kXOff)
   f32x4 acc;
   __device__ __forceinline__ explicit GemmMfma(const GemmArgs& a)
-      : x(static_cast<const uint16_t*>(a.x)), ldx(a.ldx), nb(a.nb) {}
+      : x(static_cast<const uint16_t*>(a.x)), ldx(a.ldx), nb(a.nb),
+        xa(((uintptr_t)a.x & 15u) == 0 && a.ldx % 8 == 0) {}
+  // Rows r < nb of the segment's whole tiles t .. t + 7 (16 pieces of 16
+  // bytes per row).  Slot q holds row r = q / 16, piece (q % 16) ^ r: the
+  // XOR spreads the 16 rows a consume read touches over all LDS banks.
+  __device__ __forceinline__ void stage_x(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t n) {
+    xs = xa;
+    if (!xs) return;
+    const uint32_t t = (st.start + pos0) >> 8, tiles = (n + 255) >> 8;
+    for (uint32_t i = 0; kWave * i < 16 * nb; ++i) {
+      const uint32_t q = kWave * i + lane, r = q >> 4, pc = (q & 15u) ^ r;
+      copy_to_lds16(r < nb && pc < 2 * tiles ? x + r * ldx + 16ull * t + 8 * pc : x, S.syms + kXOff + 1024 * i);
+    }
+  }
   static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) {
     const uint32_t r = lane & 15u, g = lane >> 4;
     return 32u * (g >> 1) + 2u * r + (g & 1u);
@@ -1412,7 +1491,12 @@ struct GemmMfma {
       }
       const uint4 w = combine8(E, M);
       uint4 xv = make_uint4(0u, 0u, 0u, 0u);
-      if (valid && n < nb) __builtin_memcpy(&xv, xr + 16u * (t0 + 2 * b + (g >> 1)) + 8u * (g & 1u), 16);
+      if (valid && n < nb) {
+        if (xs)
+          xv = lds16(S.syms + kXOff + 16u * (16u * n + ((4u * b + 2u * (g >> 1) + (g & 1u)) ^ n)));
+        else
+          __builtin_memcpy(&xv, xr + 16u * (t0 + 2 * b + (g >> 1)) + 8u * (g & 1u), 16);
+      }
       bf16x8 a, bb;
       __builtin_memcpy(&a, &w, 16);
       __builtin_memcpy(&bb, &xv, 16);
@@ -2117,7 +2201,7 @@ hipError_t launch_gemm_bf16(const DevBlock* blocks, uint32_t nblocks, uint32_t c
                             uint32_t* status, const ItemScratch* is, unsigned cus, hipStream_t s) {
   if (!nblocks) return hipSuccess;
   const GemmArgs ga{x, ldx, nb, y, ldy};
-  if (mfma && nb >= 8) gemm_any<GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
+  if (mfma && nb >= 2) gemm_any<GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   else gemm_valu<GemmBf16>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   return hipGetLastError();
 }

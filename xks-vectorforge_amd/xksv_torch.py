@@ -15,7 +15,7 @@ materialised.  Activations pick the path:
     (fp32 x, fp32 accumulation, python/runtime.py:267): each output is the
     fp32 sum of exact products, rel-L2 <= 1e-5 against fp64;
   * bf16 inputs take the bf16-X path in the layout of x @ W.T (bf16 MFMA
-    from 8 tokens, fp32 FMAs below), fp32 accumulation.
+    from 2 tokens, fp32 dot products for one), fp32 accumulation.
 `ResidentLinear.decode_weight` / `decode_into` are the GPU-decode load, and
 `from_archive` builds the layer from an .xksv archive's blocks.
 
