@@ -407,9 +407,11 @@ def main() -> int:
                     help="parallel32 blocks in the CPU-baseline sample (0 = every block of the archive)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemm-copies", type=int, default=4)
+    ap.add_argument("--gemm-batches", default="1,4,8,16", help="batches of the 70B-shape GEMM (comma list)")
     ap.add_argument("--only", choices=["all", "decode", "gemv", "gemm", "copy"], default="all",
                     help="run one part only (for profiler runs); prints no result line")
     args = ap.parse_args()
+    gemm_batches = tuple(int(b) for b in args.gemm_batches.split(","))
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the compressed-weight path is built and measured on a single "
               "MI355X (multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
@@ -431,7 +433,7 @@ def main() -> int:
         return 0
     if args.only == "gemm":
         for rows, cols in ((28672, 8192), (8192, 28672)):
-            g = gemm_bf16_bench(torch, lib, rows, cols, (1, 4, 8, 16), args.gemm_copies, args.steps, args.warmup,
+            g = gemm_bf16_bench(torch, lib, rows, cols, gemm_batches, args.gemm_copies, args.steps, args.warmup,
                                 stream)
             log(f"gemm bf16 {rows}x{cols}: " + ", ".join(f"b{b} {v['us_per_layer']} us" for b, v in g["batches"].items()))
         return 0
@@ -468,7 +470,7 @@ def main() -> int:
     g1 = gemv_bench(torch, lib, 14336, 4096, args.gemv_copies, args.steps, args.warmup, stream)
     g2 = gemv_bench(torch, lib, 4096, 14336, args.gemv_copies, args.steps, args.warmup, stream)
     log(f"gemv 14336x4096 {g1['us_per_layer']} us, 4096x14336 {g2['us_per_layer']} us")
-    g5 = {f"{r}x{c}": gemm_bf16_bench(torch, lib, r, c, (1, 4, 8, 16), args.gemm_copies, args.steps, args.warmup,
+    g5 = {f"{r}x{c}": gemm_bf16_bench(torch, lib, r, c, gemm_batches, args.gemm_copies, args.steps, args.warmup,
                                       stream) for r, c in ((28672, 8192), (8192, 28672))}
     log("gemm bf16 " + "; ".join(f"{k}: " + ", ".join(f"b{b} {v['us_per_layer']} us" for b, v in g["batches"].items())
                                  for k, g in g5.items()))

@@ -326,6 +326,8 @@ def test_plan_gemv_index_across_archives(hip, oracle):
         assert errs[:2] == (1, 1) and errs[2] == xksv_hip.ERR_STREAM
         keep = np.r_[0:16, 32:64]
         assert torch.equal(yr[keep], y[keep])
+        y2, errs = _gemv(plan, _upload(enc), x, rows)  # status words are stored per call, not accumulated
+        assert errs[0] == 0 and torch.equal(y2, y)
         if accepted is not None:
             back, bit, dec = accepted
             enc_a = enc.copy()

@@ -216,8 +216,7 @@ int run_block_at(uint8_t* base, const BlockLayout& L, const uint8_t* input, uint
   uint32_t* status = reinterpret_cast<uint32_t*>(base + L.status);
   if (launch_fill_u32(status, kAlign / 4, 0, nullptr) != hipSuccess) return 1;
   const DevBlock* dd = reinterpret_cast<const DevBlock*>(base + L.desc);
-  const ItemScratch is{reinterpret_cast<float*>(base + L.scratch),
-                       reinterpret_cast<uint32_t*>(base + L.scratch + kItemScratchPerBlock - 4)};
+  const ItemScratch is = item_scratch(base + L.scratch, 1);
   float* y = static_cast<float*>(out);
   if (mode == kDecode) {
     if (launch_decode(dd, 1, codec, base, static_cast<uint8_t*>(out), status, nullptr, cus, nullptr) != hipSuccess)
@@ -374,8 +373,7 @@ bool prepare_gemm(xksv_hip_plan* P, const uint8_t* arc, hipStream_t s) {
   const uint64_t item_bytes = (uint64_t)P->n_fparallel * kItemScratchPerBlock;
   if (P->n_fparallel && item_bytes <= kMaxItemMem) {
     if (hipMalloc(reinterpret_cast<void**>(&P->item_mem), item_bytes) != hipSuccess) return false;
-    P->items.partial = reinterpret_cast<float*>(P->item_mem);
-    P->items.done = reinterpret_cast<uint32_t*>(P->item_mem + (uint64_t)P->n_fparallel * (kItemScratchPerBlock - 4));
+    P->items = item_scratch(P->item_mem, P->n_fparallel);
     // Codeword index of the items (weights are static: built once, here, from
     // the archive of the first GEMM call; the kernels check it as they use it).
     // Sized for the slab rule's 32 substreams of 16 * cols / 32 symbols; an
@@ -587,8 +585,12 @@ static int plan_gemm(xksv_hip_plan* P, const void* archive, const void* x, size_
   const float* xf = static_cast<const float*>(x);
   const uint16_t* xb = static_cast<const uint16_t*>(x);
   const uint64_t M = P->rows_extent, K = P->cols;
-  if (launch_fill_u32(P->status, P->blocks.size() + kQueues, 0, s) != hipSuccess) return 1;
   const ItemScratch* items = P->item_mem ? &P->items : nullptr;
+  // The substream kernels store their blocks' status words; the other kernels
+  // OR errors in (and the decode queues count from zero).
+  if ((!items || P->n_fserial || P->n_gser || P->n_gpar) &&
+      launch_fill_u32(P->status, P->blocks.size() + kQueues, 0, s) != hipSuccess)
+    return 1;
   for (uint64_t j0 = 0; j0 < batch; j0 += kMaxFusedBatch) {
     const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxFusedBatch, batch - j0);
     hipError_t e1, e2;

@@ -1772,16 +1772,20 @@ __device__ __forceinline__ ItemLoc locate_item(const DevBlock& d, const uint8_t*
 }
 
 // Fused decode-GEMM over XKSP2 blocks of 16-row slabs, one substream per work
-// item: wave w of the grid takes items w, w + gridDim.x, ..., so all
-// resident waves share a layer's blocks x 32 substreams whatever the block
-// count.  Per item a wave decodes the substream into consumer Acc and writes
-// its kOut partial sums to the item's slot; item 0 of each block records the
-// block's substream count.  k_gemm_finish adds the slots.  The next item's
-// inputs and the header of the one after load while an item decodes.
+// item (item i = substream i % 32 of block i / 32): wave w of the grid takes
+// items w, w + gridDim.x, ..., so all resident waves share a layer's blocks x
+// 32 substreams whatever the block count, and the waves running at any one
+// time work on neighbouring items (one compact window of the archive).  Per
+// item a wave decodes the substream into consumer Acc and writes a record:
+// its partial sums (batch columns < nb) and its error word; item 0 of each
+// block records the block's substream count.  k_gemm_finish adds a block's
+// records in order and stores its status word, so no status reset precedes
+// the launch.  The next item's inputs and the header of the one after load
+// while an item decodes.
 template <class Acc>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
 k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_t* __restrict__ arc, GemmArgs ga,
-             uint32_t* __restrict__ status, ItemScratch is) {
+             ItemScratch is) {
   __shared__ Smem S;
   const uint32_t lane = lane_id(), stride = gridDim.x;
   const uint32_t nitems = nblocks * kMaxChunks;
@@ -1800,7 +1804,6 @@ k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_
   }
   for (;;) {
     const uint32_t in = i + stride, inn = in + stride, b = i / kMaxChunks, k = i % kMaxChunks;
-    const DevBlock d = blocks[b];
     ItemLoc LN{nullptr, nullptr, 0u, 0u, 0u, 0u, false};
     uint64_t hvnn = 0ull;
     if (in < nitems) {
@@ -1809,27 +1812,28 @@ k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_
       if (inn < nitems) hvnn = issue_head(arc + blocks[inn / kMaxChunks].src, blocks[inn / kMaxChunks].size, lane);
     }
     if (k == 0 && lane == 0) is.done[b] = L.err ? 0u : L.chunks;
-    if (L.err && (k == 0 || k < L.chunks)) set_status(status, d.status_slot, L.err, lane);
+    uint32_t err = L.err;  // a substream past the count carries no error of its own
     if (L.run) {
       Acc C(ga);
       C.init();
       const uint16_t* idx = is.index ? is.index + (uint64_t)i * is.index_segs * 64 : nullptr;
-      const uint32_t err = run_stream(S, lane, L.seg, L.end, L.count, L.s0, C,
-                                      NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN, idx);
+      err = run_stream(S, lane, L.seg, L.end, L.count, L.s0, C,
+                       NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN, idx);
       float* slots = reinterpret_cast<float*>(S.syms);
       for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) slots[o] = 0.f;
       wave_sync();
       C.deposit(slots, lane, L.s0);
       wave_sync();
       float* part = is.partial + (uint64_t)i * kMaxItemOut;
-      for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) part[o] = slots[o];
+      for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave)
+        if (o % Acc::kCols < ga.nb) part[o] = slots[o];
       wave_sync();
-      set_status(status, d.status_slot, err, lane);
     } else if (LN.run) {
       issue_stream(PN, LN.seg, LN.end, LN.count, lane);
       drain_loads();
       stage_inputs(S, lane, PN);
     }
+    if (lane == 0) is.err[i] = err;
     if (in >= nitems) break;
     i = in;
     L = LN;
@@ -1837,20 +1841,26 @@ k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_
   }
 }
 
-// Y of every error-free block from its items' partial sums, added in
+// Y and the status word of every block from its items' records, added in
 // substream order (fixed, so the result does not depend on which wave ran
-// which item).  One wave per block.
+// which item).  The status word is stored, not ORed: the launch needs no
+// prior reset.  One wave per block.
 template <class Acc>
 __global__ void __launch_bounds__(64) k_gemm_finish(const DevBlock* __restrict__ blocks, uint32_t nblocks,
-                                                    GemmArgs ga, const uint32_t* __restrict__ status,
-                                                    ItemScratch is) {
+                                                    GemmArgs ga, uint32_t* __restrict__ status, ItemScratch is) {
   const uint32_t lane = lane_id();
   for (uint32_t b = blockIdx.x; b < nblocks; b += gridDim.x) {
     const DevBlock d = blocks[b];
     const uint32_t chunks = is.done[b];
-    if (status[d.status_slot] || !chunks) continue;
+    const uint32_t nrec = chunks ? chunks : 1u;  // a header error is item 0's
+    uint32_t err = lane < nrec ? is.err[b * kMaxChunks + lane] : 0u;
+#pragma unroll
+    for (int m = 1; m < (int)kWave; m <<= 1) err |= __shfl_xor(err, m, kWave);
+    if (lane == 0) status[d.status_slot] = err;
+    if (err || !chunks) continue;
     const float* part = is.partial + (uint64_t)b * kMaxChunks * kMaxItemOut;
     for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) {
+      if (o % Acc::kCols >= ga.nb) continue;
       float v[kMaxChunks];
 #pragma unroll
       for (uint32_t k = 0; k < kMaxChunks; ++k) v[k] = k < chunks ? part[k * kMaxItemOut + o] : 0.f;
@@ -2159,7 +2169,7 @@ static void items_launch(hipStream_t s, const DevBlock* blocks, uint32_t nblocks
                          const GemmArgs& ga, uint32_t* status, const ItemScratch& is, unsigned cus) {
   static const unsigned per_cu = groups_per_cu(k_gemm_items<Acc>, 64);
   hipLaunchKernelGGL((k_gemm_items<Acc>), dim3(grid_for((uint64_t)nblocks * kMaxChunks, per_cu * cus)), dim3(64), 0,
-                     s, blocks, nblocks, arc, ga, status, is);
+                     s, blocks, nblocks, arc, ga, is);
   hipLaunchKernelGGL((k_gemm_finish<Acc>), dim3(grid_for(nblocks, 8 * cus)), dim3(64), 0, s, blocks, nblocks, ga,
                      status, is);
 }

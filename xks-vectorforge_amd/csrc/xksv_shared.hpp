@@ -43,8 +43,8 @@ constexpr uint32_t kMaxChunks = 32;
 // are split into column groups by the host.
 constexpr uint32_t kMaxFusedBatch = 16;
 // Fused GEMM over XKSP2 blocks by substream ("items"): per block, kMaxChunks
-// partial-sum slots of kMaxItemOut floats and the block's substream count
-// (written by the item kernel; 0 = header error).
+// records (kMaxItemOut partial sums and an error word each) and the block's
+// substream count (written by the item kernel; 0 = header error).
 constexpr uint32_t kMaxItemOut = 16 * kMaxFusedBatch;
 // Codeword index of the fused XKSP2 items (a load-time sidecar of static
 // weights): per item, `index_segs` segments of kIdxSegSyms symbols, each 64
@@ -57,10 +57,19 @@ constexpr uint32_t kIdxSegSyms = 64 * kIdxLaneSyms;
 constexpr uint16_t kIdxNone = 0xFFFF;
 struct ItemScratch {
   float* partial;         // [blocks][kMaxChunks][kMaxItemOut]
+  uint32_t* err;          // [blocks][kMaxChunks]
   uint32_t* done;         // [blocks]
   const uint16_t* index;  // [items][index_segs][64], or nullptr
   uint32_t index_segs;
 };
-constexpr uint64_t kItemScratchPerBlock = (uint64_t)kMaxChunks * kMaxItemOut * 4 + 4;
+constexpr uint64_t kItemScratchPerBlock = (uint64_t)kMaxChunks * kMaxItemOut * 4 + kMaxChunks * 4 + 4;
+// ItemScratch over `base` for `nblocks` blocks (kItemScratchPerBlock bytes each).
+inline ItemScratch item_scratch(uint8_t* base, uint64_t nblocks) {
+  ItemScratch is{};
+  is.partial = reinterpret_cast<float*>(base);
+  is.err = reinterpret_cast<uint32_t*>(base + nblocks * kMaxChunks * kMaxItemOut * 4);
+  is.done = reinterpret_cast<uint32_t*>(base + nblocks * (kMaxChunks * kMaxItemOut * 4 + kMaxChunks * 4));
+  return is;
+}
 
 }  // namespace xksv
