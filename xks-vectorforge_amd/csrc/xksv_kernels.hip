@@ -571,10 +571,14 @@ __device__ __forceinline__ uint32_t step2(const Smem& S, uint32_t& p, uint32_t& 
                                           uint32_t& w2, uint32_t maxlen, uint32_t& dead) {
   const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
   uint32_t e = S.t.f.lut2[win >> (32 - kLutBits)];
-  if (e == kLongMark) {
-    const uint32_t lc = long_code(S, win, maxlen);  // (len << 8) | symbol: no second symbol, len1 0
-    dead |= lc == 0;
-    e = lc ? lc : kDeadMark;
+  // A wave-uniform test first: the common step then takes no exec-mask
+  // save/restore and no taken branch.
+  if (__builtin_expect(__ballot(e == kLongMark) != 0, 0)) {
+    if (e == kLongMark) {
+      const uint32_t lc = long_code(S, win, maxlen);  // (len << 8) | symbol: no second symbol, len1 0
+      dead |= lc == 0;
+      e = lc ? lc : kDeadMark;
+    }
   }
   p += (e >> 8) & 127u;
   slide(S, p, wi, w0, w1, w2);
@@ -991,10 +995,12 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
     while (n < k) {
       const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
       uint32_t en = S.t.f.lut2[win >> (32 - kLutBits)];
-      if (en == kLongMark) {
-        const uint32_t lc = long_code(S, win, maxlen);
-        d |= lc == 0;
-        en = lc ? lc : kDeadMark;
+      if (__builtin_expect(__ballot(en == kLongMark) != 0, 0)) {
+        if (en == kLongMark) {
+          const uint32_t lc = long_code(S, win, maxlen);
+          d |= lc == 0;
+          en = lc ? lc : kDeadMark;
+        }
       }
       const uint32_t pair = (en >> 15) & 1u, two = pair & (n + 1 < k ? 1u : 0u);
       o[n] = (uint8_t)en;
