@@ -105,7 +105,12 @@ struct alignas(16) Smem {
 };
 // X columns of one indexed segment, staged for the fused GEMM consumers: in
 // the symbol buffer past the segment's symbols and the lanes' junk bytes.
-constexpr uint32_t kXOff = kIdxSegSyms + 256;
+// Lane slots of the indexed walk: kIdxLaneSyms symbols, then padding that is
+// the lane's junk byte; 9 dwords, odd, so that lanes storing their n-th
+// symbol together hit distinct LDS banks.
+constexpr uint32_t kIdxStride = kIdxLaneSyms + 4;
+static_assert(kIdxStride % 8 == 4, "indexed lane slots: odd dword stride");
+constexpr uint32_t kXOff = kWave * kIdxStride;
 constexpr uint32_t kXBytes = 4096;
 static_assert(kXOff + kXBytes <= kSymsBytes, "staged X must fit the symbol buffer");
 
@@ -671,11 +676,14 @@ __device__ __forceinline__ void issue_stream(StreamIn& P, const uint8_t* seg, co
     P.bits.drop = 16;
   }
 }
+// N < kSmWin: only the first N window entries are loaded (a consume call
+// that sees at most N * 64 units); the rest are constant zeros.
+template <uint32_t N = kSmWin>
 __device__ __forceinline__ void issue_sm(SmWin& W, const uint8_t* sm, uint32_t pos0, uint32_t count, uint32_t lu) {
 #pragma unroll
   for (uint32_t i = 0; i < kSmWin; ++i) {
     const uint32_t p = pos0 + 8 * (lu + kWave * i);
-    W.v[i] = p + 8 <= count ? ldg64(sm + p) : 0ull;
+    W.v[i] = i < N && p + 8 <= count ? ldg64(sm + p) : 0ull;
   }
 }
 // The stream after the current one (seg == nullptr: none); its inputs are
@@ -702,6 +710,16 @@ __device__ __forceinline__ void drain_loads() { __builtin_amdgcn_s_waitcnt(0x0F7
 // copy is an outstanding load until drain_loads().
 __device__ __forceinline__ void copy_to_lds16(const void* src, uint8_t* dst) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+// The 8 exponents of unit u (8 consecutive symbols) of a consume call:
+// compacted runs (decode_fast) hold them at byte 8u; the indexed walk's lane
+// slots at kIdxStride (u / 4) + 8 (u % 4), dword aligned.
+template <bool kIx>
+__device__ __forceinline__ uint64_t unit_exps(const uint8_t* syms, uint32_t u) {
+  static_assert(kIdxStride == 36, "slot offset below: 36 (u / 4) + 8 (u % 4) = 8 u + 4 (u / 4)");
+  const uint32_t off = kIx ? 8u * u + (u & ~3u) : 8u * u;
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(syms + off);
+  return (uint64_t)q[0] | ((uint64_t)q[1] << 32);
 }
 // 16 bytes of LDS through an LDS pointer: a read that the compiler could
 // otherwise merge with a global read of the other branch into one FLAT load.
@@ -977,17 +995,17 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
     const bool more = pos0 + n_s < st.count;
     if (more && lane < kStreamLanes) cur = fetch16(st.bits + (nextbit >> 3) + 16 * lane, bend);
     SmWin W;
-    issue_sm(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
+    issue_sm<kIdxSegSyms / 8 / kWave>(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
     C.stage_x(S, lane, st, pos0, n_s);  // lands in LDS during the walk
     // The staged buffer starts at byte segbit >> 3 (its bit 0 after the zero dword).
     const uint32_t base = (uint32_t)(segbit & 7u), limit = base + want;
     uint32_t p = base + rel, n = 0, d = 0, wi, w0, w1, w2;
     load_window(S, p, wi, w0, w1, w2);
-    lds_bytes const o = as_lds(S.syms + kIdxLaneSyms * lane);
+    lds_bytes const o = as_lds(S.syms + kIdxStride * lane);
     // A pair whose second symbol is not wanted (the lane's last symbol) stores
     // it into the lane's own junk byte past the segment's symbols, so the
     // step has no branch around the store.
-    lds_bytes const junk = as_lds(S.syms + kIdxSegSyms + lane);
+    lds_bytes const junk = o + kIdxLaneSyms;
     // One exit condition: a lane walks exactly k symbols.  A path on wrong
     // offsets (a stale index) advances at most 127 bits per step for at most
     // kIdxLaneSyms steps, which stays inside this wave's LDS block, and fails
@@ -1023,7 +1041,7 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
       stage_inputs(S, lane, PN);
       staged = true;
     }
-    C.consume(S, lane, st, pos0, n_s, fin, W);
+    C.template consume<true>(S, lane, st, pos0, n_s, fin, W);  // symbols in the lane slots
     wave_sync();
     pos0 += n_s;
     segbit = nextbit;
@@ -1178,6 +1196,7 @@ struct Writer {
     const uint32_t col = 16u * (T - band * tpb) + 8u * (U & 1u);
     __builtin_memcpy(out + 2ull * (row * (uint32_t)cols + col), &w, 16);
   }
+  template <bool kIx = false>  // never fed by the indexed walk
   __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final,
                               const SmWin& W) {
     if (!aligned) {
@@ -1265,9 +1284,9 @@ struct GemmF32 {
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = 0.f;
   }
+  template <bool kIx>
   __device__ __forceinline__ void unit(const Smem& S, const Stream& st, uint32_t pos0, uint32_t u, uint64_t M) {
-    uint64_t E;
-    __builtin_memcpy(&E, S.syms + 8 * u, 8);
+    const uint64_t E = unit_exps<kIx>(S.syms, u);
     const uint4 w = combine8(E, M);
     const uint32_t U = ((st.start + pos0) >> 3) + u;
     const uint64_t col = 16ull * (U >> 5) + 8u * (U & 1u);
@@ -1304,6 +1323,8 @@ struct GemmF32 {
       }
     }
   }
+  // kIx: the symbols are in the indexed walk's lane slots.
+  template <bool kIx = false>
   __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0,
                                               uint32_t avail, bool final, const SmWin& W) {
     const uint32_t take = final ? avail : (avail & ~255u);
@@ -1311,10 +1332,10 @@ struct GemmF32 {
 #pragma unroll
     for (uint32_t i = 0; i < kSmWin; ++i) {
       const uint32_t u = lane + kWave * i;
-      if (u < units) unit(S, st, pos0, u, W.v[i]);
+      if (u < units) unit<kIx>(S, st, pos0, u, W.v[i]);
     }
     for (uint32_t u = lane + kSmWin * kWave; u < units; u += kWave)
-      unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
+      unit<kIx>(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
     return take;
   }
   // Four lanes share each row: with s = (stream start / 8) % 2, lane l and
@@ -1386,9 +1407,9 @@ struct GemmBf16 {
     __builtin_memcpy(&vb, &b, 4);
     return __builtin_amdgcn_fdot2_f32_bf16(va, vb, c, false);
   }
+  template <bool kIx>
   __device__ __forceinline__ void unit(const Smem& S, const Stream& st, uint32_t pos0, uint32_t u, uint64_t M) {
-    uint64_t E;
-    __builtin_memcpy(&E, S.syms + 8 * u, 8);
+    const uint64_t E = unit_exps<kIx>(S.syms, u);
     const uint4 w = combine8(E, M);
     const uint32_t U = ((st.start + pos0) >> 3) + u;
     const uint64_t col = 16ull * (U >> 5) + 8u * (U & 1u);
@@ -1409,6 +1430,8 @@ struct GemmBf16 {
       }
     }
   }
+  // kIx: the symbols are in the indexed walk's lane slots.
+  template <bool kIx = false>
   __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0,
                                               uint32_t avail, bool final, const SmWin& W) {
     const uint32_t take = final ? avail : (avail & ~255u);
@@ -1416,10 +1439,10 @@ struct GemmBf16 {
 #pragma unroll
     for (uint32_t i = 0; i < kSmWin; ++i) {
       const uint32_t u = lane + kWave * i;
-      if (u < units) unit(S, st, pos0, u, W.v[i]);
+      if (u < units) unit<kIx>(S, st, pos0, u, W.v[i]);
     }
     for (uint32_t u = lane + kSmWin * kWave; u < units; u += kWave)
-      unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
+      unit<kIx>(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
     return take;
   }
   __device__ __forceinline__ void deposit(float* slots, uint32_t lane, uint32_t s0) {
@@ -1481,6 +1504,8 @@ struct GemmMfma {
     if (j < a.nb) a.y[j * a.ldy + dst + r] = v;
   }
   __device__ __forceinline__ void init() { acc = f32x4{0.f, 0.f, 0.f, 0.f}; }
+  // kIx: the symbols are in the indexed walk's lane slots.
+  template <bool kIx = false>
   __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0,
                                               uint32_t avail, bool final, const SmWin& W) {
     const uint32_t take = final ? avail : (avail & ~255u);  // whole tiles for fitting streams
@@ -1492,7 +1517,7 @@ struct GemmMfma {
       const bool valid = u < units;  // an odd tile count leaves the last pair half empty
       uint64_t E = 0, M = 0;
       if (valid) {
-        __builtin_memcpy(&E, S.syms + 8 * u, 8);
+        E = unit_exps<kIx>(S.syms, u);
         M = b < kSmWin ? W.v[b] : ldg64(st.sm + pos0 + 8 * u);
       }
       const uint4 w = combine8(E, M);
