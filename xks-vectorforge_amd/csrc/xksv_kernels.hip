@@ -1855,9 +1855,10 @@ k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_
       wave_sync();
       C.deposit(slots, lane, L.s0);
       wave_sync();
+      // Live batch columns only, packed: row r, column j < nb at r * nb + j.
       float* part = is.partial + (uint64_t)i * kMaxItemOut;
       for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave)
-        if (o % Acc::kCols < ga.nb) part[o] = slots[o];
+        if (o % Acc::kCols < ga.nb) part[(o / Acc::kCols) * ga.nb + o % Acc::kCols] = slots[o];
       wave_sync();
     } else if (LN.run) {
       issue_stream(PN, LN.seg, LN.end, LN.count, lane);
@@ -1890,15 +1891,14 @@ __global__ void __launch_bounds__(64) k_gemm_finish(const DevBlock* __restrict__
     if (lane == 0) status[d.status_slot] = err;
     if (err || !chunks) continue;
     const float* part = is.partial + (uint64_t)b * kMaxChunks * kMaxItemOut;
-    for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) {
-      if (o % Acc::kCols >= ga.nb) continue;
+    for (uint32_t o = lane; o < 16 * ga.nb; o += kWave) {  // packed records: row o / nb, column o % nb
       float v[kMaxChunks];
 #pragma unroll
       for (uint32_t k = 0; k < kMaxChunks; ++k) v[k] = k < chunks ? part[k * kMaxItemOut + o] : 0.f;
       float sum = 0.f;
 #pragma unroll
       for (uint32_t k = 0; k < kMaxChunks; ++k) sum += v[k];
-      Acc::store(ga, d.dst, o / Acc::kCols, o % Acc::kCols, sum);
+      Acc::store(ga, d.dst, o / ga.nb, o % ga.nb, sum);
     }
   }
 }
