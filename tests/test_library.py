@@ -106,12 +106,14 @@ def test_kernels_address_lds_without_flat_instructions(tmp_path):
     flat = [ln for ln in text.splitlines() if re.match(r"\s+flat_", ln)]
     assert not flat, flat[:5]
     assert "_ZN4xksv12_GLOBAL__N_117k_decode_parallel" in text
-    # Private (scratch) memory: none in the decode kernels; the fused GEMM item
-    # kernels, at their register limit, may spill a few words at item level.
+    # Private (scratch) memory: none in the per-wave decode kernels; the fused
+    # GEMM item kernels and the workgroup serial decode, at their register
+    # limit, may spill a few words outside the walk loops.
     kernels = re.findall(r"\.name:\s+(\S+)\n(?:.*\n)*?\s+\.private_segment_fixed_size:\s+(\d+)", text)
     assert kernels
     for name, size in kernels:
-        assert int(size) == 0 or ("k_gemm_items" in name and int(size) <= 16), (name, size)
+        assert int(size) == 0 or (("k_gemm_items" in name or "k_decode_serial_wg" in name) and int(size) <= 16), \
+            (name, size)
 
 
 @pytest.mark.parametrize("codec", [1, 2])

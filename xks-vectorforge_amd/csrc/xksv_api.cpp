@@ -192,7 +192,9 @@ BlockLayout block_layout(uint64_t size, uint32_t codec, uint64_t rows, uint64_t 
   const uint64_t n = rows * cols;
   const bool generic_gemm = mode != kDecode && !fused.unit;
   const bool items = mode != kDecode && !generic_gemm && codec == kCodecParallel;
-  const uint64_t scratch_size = generic_gemm ? n * 2 : items ? kItemScratchPerBlock : 0;
+  uint32_t grid = 0, cap = 0;
+  const uint64_t serial = mode == kDecode && codec == kCodecSerial ? serial_wg_scratch(1, n, 1, &grid, &cap) : 0;
+  const uint64_t scratch_size = generic_gemm ? n * 2 : items ? kItemScratchPerBlock : serial;
   BlockLayout L;
   L.desc = 0;
   L.status = align_up(L.desc + 2 * sizeof(DevBlock), kAlign);
@@ -218,7 +220,13 @@ int run_block_at(uint8_t* base, const BlockLayout& L, const uint8_t* input, uint
   const DevBlock* dd = reinterpret_cast<const DevBlock*>(base + L.desc);
   const ItemScratch is = item_scratch(base + L.scratch, 1);
   float* y = static_cast<float*>(out);
-  if (mode == kDecode) {
+  if (mode == kDecode && codec == kCodecSerial) {  // one workgroup for the block
+    uint32_t grid = 0, cap = 0;
+    (void)serial_wg_scratch(1, rows * cols, 1, &grid, &cap);
+    if (launch_decode_serial_wg(dd, 1, base, static_cast<uint8_t*>(out), status, base + L.scratch, cap, grid,
+                                nullptr) != hipSuccess)
+      return 1;
+  } else if (mode == kDecode) {
     if (launch_decode(dd, 1, codec, base, static_cast<uint8_t*>(out), status, nullptr, cus, nullptr) != hipSuccess)
       return 1;
   } else if (!generic_gemm) {
@@ -271,6 +279,8 @@ struct xksv_hip_plan {
   uint32_t n_fserial = 0, n_fparallel = 0, n_gser = 0, n_gpar = 0, n_generic = 0, n_graw = 0;
   bool tile_parallel = false;  // parallel32 slabs split into whole-tile substreams (MFMA consumer)
   uint8_t* scratch = nullptr;
+  uint8_t* serial_scratch = nullptr;  // workgroup-scale serial decode (k_decode_serial_wg)
+  uint32_t serial_grid = 0, serial_cap = 0;
   uint8_t* item_mem = nullptr;  // ItemScratch of the fused XKSP2 list (none: workgroup-per-block kernels)
   uint8_t* digests = nullptr;   // verification: SHA-256 per block, table order (allocated on first use)
   uint16_t* index = nullptr;    // codeword index of the fused XKSP2 items (ItemScratch::index)
@@ -521,6 +531,14 @@ int xksv_hip_plan_create(const xksv_hip_block* blocks, size_t nblocks, uint64_t 
   }
   ok = ok && upload(ser, &P->d_serial) && upload(par, &P->d_parallel) && upload(raw, &P->d_raw);
   P->n_serial = (uint32_t)ser.size();
+  if (ok && !ser.empty()) {  // serial blocks decode a workgroup each
+    uint64_t max_elems = 0;
+    for (const DevBlock& d : ser) max_elems = std::max<uint64_t>(max_elems, d.rows * d.cols);
+    const DeviceInfo* di = current_device(nullptr);
+    const uint64_t bytes =
+        di ? serial_wg_scratch(P->n_serial, max_elems, (unsigned)di->cus, &P->serial_grid, &P->serial_cap) : 0;
+    ok = di && hipMalloc(reinterpret_cast<void**>(&P->serial_scratch), bytes) == hipSuccess;
+  }
   P->n_parallel = (uint32_t)par.size();
   P->n_raw = (uint32_t)raw.size();
   P->h_status.assign(nblocks ? nblocks : 1, 0);
@@ -543,7 +561,8 @@ int xksv_hip_plan_destroy(xksv_hip_plan* P) {
   if (P->device >= 0 && cur != P->device) (void)hipSetDevice(P->device);
   for (void* p : {(void*)P->d_serial, (void*)P->d_parallel, (void*)P->d_raw, (void*)P->status, (void*)P->g_fserial,
                   (void*)P->g_fparallel, (void*)P->g_gser, (void*)P->g_gpar, (void*)P->g_gplain, (void*)P->g_raw,
-                  (void*)P->scratch, (void*)P->item_mem, (void*)P->digests, (void*)P->index})
+                  (void*)P->scratch, (void*)P->item_mem, (void*)P->digests, (void*)P->index,
+                  (void*)P->serial_scratch})
     if (p) (void)hipFree(p);
   if (cur >= 0 && cur != P->device) (void)hipSetDevice(cur);
   delete P;
@@ -562,8 +581,8 @@ int xksv_hip_plan_decode(xksv_hip_plan* P, const void* archive, void* out, uint6
   if (launch_decode(P->d_parallel, P->n_parallel, kCodecParallel, arc, o, P->status, queue, (unsigned)di->cus, s) !=
       hipSuccess)
     return 1;
-  if (launch_decode(P->d_serial, P->n_serial, kCodecSerial, arc, o, P->status, queue + 1, (unsigned)di->cus, s) !=
-      hipSuccess)
+  if (launch_decode_serial_wg(P->d_serial, P->n_serial, arc, o, P->status, P->serial_scratch, P->serial_cap,
+                              P->serial_grid, s) != hipSuccess)
     return 1;
   if (launch_copy_raw(P->d_raw, P->n_raw, arc, o, s) != hipSuccess) return 1;
   return 0;

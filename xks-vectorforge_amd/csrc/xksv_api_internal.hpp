@@ -54,6 +54,12 @@ int run_block_at(uint8_t* base, const BlockLayout& L, const uint8_t* input, uint
 // `queue` (optional) is a zeroed counter the decode waves claim blocks from.
 hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc, uint8_t* out,
                          uint32_t* status, uint32_t* queue, unsigned cus, hipStream_t s);
+// Serial blocks decoded by a workgroup each (k_decode_serial_wg): scratch
+// bytes for `nblocks` blocks of at most `max_elems` elements; sets the grid
+// and the per-wave region size the launch takes.
+uint64_t serial_wg_scratch(uint32_t nblocks, uint64_t max_elems, unsigned cus, uint32_t* grid, uint32_t* cap);
+hipError_t launch_decode_serial_wg(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint8_t* out,
+                                   uint32_t* status, uint8_t* scratch, uint32_t cap, uint32_t grid, hipStream_t s);
 hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
                            const ItemScratch* is, unsigned cus, hipStream_t s);

@@ -48,6 +48,7 @@ constexpr uint32_t kLongMark = kLongLen << 8;
 constexpr uint32_t kMaxLenFast = 32;
 constexpr uint32_t kSlowSeg = 4096;                 // symbols per bit-serial segment (multiple of 256)
 constexpr uint64_t kMagicXKSP2 = 0x0000003250534B58ull;  // "XKSP2\0\0\0" little-endian
+constexpr uint32_t kSerialWaves = 12;               // waves per serial block (workgroup-scale decode)
 // Longest segment of an indexed item (fused GEMM codeword index), in code
 // bits: the segment, its start's bit offset within its first byte, the
 // register window's lookahead (96 bits) and a dead path's jump (kLongLen)
@@ -753,6 +754,27 @@ __device__ __forceinline__ void stage_inputs(Smem& S, uint32_t lane, const Strea
   wave_sync();
 }
 
+// A sub-range of a stream (workgroup-scale serial decode): the codewords that
+// start in [start_bit, end_bit).  With `spec`, start_bit is not known to be a
+// codeword boundary: lane 0 walks its first chunk from up to kSync bits
+// earlier, like the other lanes, and `first` returns the first codeword start
+// at or past start_bit on that path (kNoStart64 when the path died before it).
+// `exit` returns the first codeword start at or past end_bit and `count` the
+// symbols decoded.  Only a range that ends the stream checks the trailing bits.
+constexpr uint64_t kNoStart64 = ~0ull;
+struct Range {
+  uint64_t end_bit;
+  bool spec;
+  uint64_t first, exit;
+  uint32_t count;
+};
+// Consumers that do not read the sign/mantissa bytes (SmUse false) get no
+// window loads.
+template <class C>
+struct SmUse {
+  static constexpr bool value = true;
+};
+
 // Decode one stream with the fast tables; the consumer receives the
 // exponents in stream order.  `first` holds the stream's first 784 code
 // bytes; later segments are loaded one segment ahead.  Returns error bits.
@@ -764,12 +786,16 @@ template <class Cons>
 // stream decoded from its start has its first bytes staged with its inputs.
 __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen,
                                                 const uint8_t* blk_end, Cons& C, const StreamIn& PN, bool next,
-                                                uint64_t start_bit = 0, uint32_t start_pos = 0) {
+                                                uint64_t start_bit = 0, uint32_t start_pos = 0,
+                                                Range* R = nullptr) {
   const uint64_t nbits = st.nbits;
+  const uint64_t end = R ? R->end_bit : nbits;  // decode the codewords that start before `end`
+  bool spec = R && R->spec;
   const uint8_t* bend = st.bits + ((nbits + 7) >> 3);
   if (bend > blk_end) bend = blk_end;
   uint8_t* const region = S.syms + kCarry + lane * kRegion;
-  uint64_t S0 = start_bit & ~7ull, true_pos = start_bit;
+  // A speculative start stages from kSync bits earlier, so lane 0 can walk in.
+  uint64_t S0 = (spec ? start_bit - (start_bit < kSync ? start_bit : (uint64_t)kSync) : start_bit) & ~7ull, true_pos = start_bit;
   uint32_t carry = 0, pos0 = start_pos, entry = (uint32_t)(start_bit - S0), err = 0;
   // Chunk size: the stream is cut into the fewest segments of at most kSegBits
   // bits, and each segment evenly over the 64 lanes, so that every segment --
@@ -777,19 +803,19 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
   // follows its longest chunk, so a stream of 1.1 segments at fixed 96-bit
   // chunks would cost two full segments.
   uint32_t chunk = kChunk;
-  if (nbits > S0) {
-    const uint64_t nseg = (nbits - S0 + kSegBits - 1) / kSegBits;
-    chunk = (uint32_t)((nbits - S0 + kWave * nseg - 1) / (kWave * nseg));
+  if (end > S0) {
+    const uint64_t nseg = (end - S0 + kSegBits - 1) / kSegBits;
+    chunk = (uint32_t)((end - S0 + kWave * nseg - 1) / (kWave * nseg));
   }
   const uint32_t segbits = kWave * chunk;
   Fetch16 cur;
   cur.v = make_uint4(0u, 0u, 0u, 0u);
   cur.drop = 16;
-  const bool resume = start_bit != 0 || start_pos != 0;
+  const bool resume = start_bit != 0 || start_pos != 0 || spec;
   if (resume && lane < kStreamLanes) cur = fetch16(st.bits + (S0 >> 3) + 16 * lane, bend);
   bool stage_top = resume;
   bool staged = false;
-  while (true_pos < nbits) {
+  while (true_pos < end) {
     if (stage_top) {  // a stream's first segment was staged with its inputs
       stage_bits(S, lane, cur.value());
       wave_sync();
@@ -797,21 +823,37 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
     stage_top = true;
     // Next segment's code bytes and this segment's sign/mantissa window go
     // out now and land while the segment decodes.
-    if (S0 + segbits < nbits && lane < kStreamLanes)
+    if (S0 + segbits < end && lane < kStreamLanes)
       cur = fetch16(st.bits + ((S0 + segbits) >> 3) + 16 * lane, bend);
     SmWin W;
-    issue_sm(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
-    const uint64_t left = nbits - S0;
+    if constexpr (SmUse<Cons>::value) issue_sm(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
+    const uint64_t left = end - S0;
     const uint32_t lim_bits = left < segbits ? (uint32_t)left : segbits;
-    const uint32_t cs = lane * chunk;
+    // The lanes' chunks tile [0, lim_bits); after a speculative start they
+    // tile [entry, lim_bits) instead (the bits before the entry belong to the
+    // previous range), in chunks no longer than `chunk`.
+    const uint32_t g0 = spec ? min(entry, lim_bits) : 0u;
+    const uint32_t cw = spec ? max(1u, (lim_bits - g0 + kWave - 1) / kWave) : chunk;
+    const uint32_t cs = g0 + lane * cw;
     const bool active = cs < lim_bits;
-    const uint32_t ce = active ? min(cs + chunk, lim_bits) : cs;
-    // Lane 0 starts at the true entry; the others kSync bits before their
-    // chunk, or at the entry when that is closer (a true start: small chunks
-    // of a short stream).  An inactive lane's empty range gives f = ex = cs,
+    const uint32_t ce = active ? min(cs + cw, lim_bits) : cs;
+    // Lane 0 starts at the true entry (speculative: at the segment's first
+    // staged bit); the others kSync bits before their chunk, or at the entry
+    // when that is closer.  An inactive lane's empty range gives f = ex = cs,
     // cnt = 0.
     Path P;
-    decode_chunk(S, !active ? cs : cs > entry + kSync ? cs - kSync : entry, cs, ce, region, maxlen, P);
+    decode_chunk(S, !active ? cs : lane == 0 ? (spec ? 0u : entry) : cs > entry + kSync ? cs - kSync : entry, cs, ce,
+                 region, maxlen, P);
+    if (spec) {  // the range's first codeword on lane 0's path: trusted here, checked by the caller
+      const uint32_t f0 = rdlane(P.f, 0);
+      R->first = f0 == kNoStart ? kNoStart64 : S0 + f0;
+      if (f0 == kNoStart) {
+        err = kErrStream;
+        break;
+      }
+      entry = f0;
+      spec = false;
+    }
     // Resolve: lane i is on the true path when its first start equals its
     // predecessor's exit and the predecessor is.  Lanes that fail re-decode
     // from that exit (rare: a path that did not resynchronise within kSync).
@@ -914,7 +956,7 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
       wave_sync();
     }
     const uint32_t avail = carry + total;
-    const bool fin = S0 + seg_exit >= nbits;  // last segment: hand over everything
+    const bool fin = S0 + seg_exit >= end;  // last segment: hand over everything
     drain_loads();
     if (fin && next) {  // this stream is done with the segment buffer
       stage_inputs(S, lane, PN);
@@ -934,7 +976,13 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
     entry = seg_exit - segbits;
     S0 += segbits;
   }
-  if (!err && (true_pos != nbits || (uint64_t)pos0 + carry != st.count)) err = kErrStream;
+  if (R) {
+    R->exit = true_pos;
+    R->count = pos0 + carry;
+    if (!err && end == nbits && true_pos != nbits) err = kErrStream;  // trailing bits
+  } else if (!err && (true_pos != nbits || (uint64_t)pos0 + carry != st.count)) {
+    err = kErrStream;
+  }
   wave_sync();
   if (next && !staged) {  // left early (an error): hand the next stream's inputs on anyway
     drain_loads();
@@ -1238,6 +1286,74 @@ struct Writer {
     return take;
   }
 };
+
+// Exponents of a sub-range in stream order, as bytes at dst[0 ...] (first
+// pass of the workgroup-scale serial decode).  16-byte stores; a call that
+// would pass `cap` bytes sets `overflow` and stores nothing.
+struct ScratchWriter {
+  uint8_t* dst;
+  uint32_t cap;
+  bool overflow = false;
+  bool xs = false;  // no activations
+  __device__ __forceinline__ void stage_x(Smem&, uint32_t, const Stream&, uint32_t, uint32_t) {}
+  static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) { return lane; }
+  template <bool kIx = false>
+  __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream&, uint32_t pos0, uint32_t avail,
+                                              bool final, const SmWin&) {
+    const uint32_t take = final ? avail : (avail & ~255u);
+    if ((uint64_t)pos0 + take + 16 > cap) {
+      overflow = true;
+      return take;
+    }
+    for (uint32_t o = 16 * lane; o < take; o += 16 * kWave) {
+      const uint4 v = lds16(S.syms + o);
+      __builtin_memcpy(dst + pos0 + o, &v, 16);
+    }
+    return take;
+  }
+};
+template <>
+struct SmUse<ScratchWriter> {
+  static constexpr bool value = false;
+};
+
+// Second pass of the workgroup-scale serial decode: tiled positions
+// [P, P + n) of a slab, whose exponents are the bytes at src (4-byte aligned,
+// readable 8 bytes past n), become BF16 outputs.  On unit-aligned slabs the
+// units of 8 positions wholly inside go out as 16-byte stores; the partial
+// units at either end, and every position of other slabs, one element at a
+// time.  A unit's exponents sit at src offset 8U - P, misaligned by the same
+// d = (8 u0 - P) % 4 for every unit, and are funnel-shifted out of 3 dwords.
+__device__ __forceinline__ void place_range(const uint8_t* src, const Stream& st, uint32_t P, uint32_t n,
+                                            uint8_t* out, uint64_t rows, uint64_t cols, bool aligned, uint32_t lane) {
+  const uint32_t u0 = aligned ? (P + 7) >> 3 : 0u, u1 = aligned ? (P + n) >> 3 : 0u;
+  const bool units = u0 < u1;
+  const uint32_t lo_end = units ? 8 * u0 : P + n, hi_beg = units ? 8 * u1 : P + n;
+  // element-wise: [P, lo_end) and [hi_beg, P + n)
+  const uint32_t n_lo = lo_end - P, n_el = n_lo + (P + n - hi_beg);
+  for (uint32_t i = lane; i < n_el; i += kWave) {
+    const uint32_t t = i < n_lo ? P + i : hi_beg + (i - n_lo);
+    const uint32_t e = src[t - P], sm = st.sm[t];
+    const uint16_t w = (uint16_t)(((sm & 0x80u) << 8) | (e << 7) | (sm & 0x7fu));
+    uint32_t row, col;
+    tile_to_rc(t, (uint32_t)rows, (uint32_t)cols, row, col);
+    __builtin_memcpy(out + 2ull * ((uint64_t)row * cols + col), &w, 2);
+  }
+  if (!units) return;
+  const uint32_t d8 = 8u * ((8u * u0 - P) & 3u), tpb = (uint32_t)(cols / 16);
+  for (uint32_t U = u0 + lane; U < u1; U += kWave) {
+    const uint32_t j = 8u * U - P;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(src + (j & ~3u));
+    const uint32_t a = q[0], b = q[1], c = q[2];
+    const uint64_t E = (uint64_t)__builtin_amdgcn_alignbit(b, a, d8) |
+                       ((uint64_t)__builtin_amdgcn_alignbit(c, b, d8) << 32);
+    const uint4 w = combine8(E, ldg64(st.sm + 8ull * U));
+    const uint32_t T = U >> 5, band = rows == 16 ? 0u : T / tpb;
+    const uint32_t row = 16u * band + ((U >> 1) & 15u);
+    const uint32_t col = 16u * (T - band * tpb) + 8u * (U & 1u);
+    __builtin_memcpy(out + 2ull * ((uint64_t)row * cols + col), &w, 16);
+  }
+}
 
 // Fused GEMM consumers.  Each one accumulates one wave's share of a 16-row
 // slab's Y = W X and, after every stream, adds it into the wave's LDS slots
@@ -1685,6 +1801,118 @@ k_decode_serial(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uin
       stage_inputs(S, lane, PN);
     }
     set_status(status, d.status_slot, err, lane);
+  }
+}
+
+// Serial-codec blocks at workgroup scale: kSerialWaves waves share a block.
+// Pass 1: wave w decodes the codewords that start in its share of the code
+// bits, [nbits w / W, nbits (w + 1) / W), from a speculative entry (as a lane
+// enters its chunk) into its scratch region, and records its first codeword
+// start, its exit and its count.  Then, wave by wave, a range whose first
+// start is not its predecessor's exit is decoded again from that exit; a
+// range in which no codeword starts passes the exit on.  The block then
+// follows the reference's serial walk: a range's decode error counts once its
+// start is proven, the counts must add up to the element count, and the last
+// range must end on the stream's last bit.  Pass 2: each wave places its
+// symbols at the sum of the counts before it.  A block whose stream is short,
+// invalid, needs the bit-serial path, or overflows a scratch region is
+// decoded by wave 0 alone.
+struct SerialPart {
+  uint64_t first, exit;
+  uint32_t count, err;
+};
+__global__ void __launch_bounds__(64 * kSerialWaves)
+k_decode_serial_wg(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_t* __restrict__ arc,
+                   uint8_t* __restrict__ out, uint32_t* __restrict__ status, uint8_t* __restrict__ scratch,
+                   uint32_t cap) {
+  __shared__ Smem SS[kSerialWaves];
+  __shared__ SerialPart R[kSerialWaves];
+  __shared__ uint32_t over;
+  const uint32_t lane = lane_id(), w = threadIdx.x / kWave;
+  Smem& S = SS[w];
+  uint8_t* const mine = scratch + ((uint64_t)blockIdx.x * kSerialWaves + w) * cap;
+  for (uint32_t b = blockIdx.x; b < nblocks; b += gridDim.x) {
+    if (threadIdx.x == 0) over = 0;
+    __syncthreads();
+    const DevBlock d = blocks[b];
+    if (d.size < 272 || !d.rows || !d.cols || d.cols > ~0ull / d.rows || d.rows * d.cols > kMaxBlockElems) {
+      if (w == 0) set_status(status, d.status_slot, d.size < 272 || !d.rows || !d.cols || d.cols > ~0ull / d.rows
+                                                        ? kErrHeader : kErrShape, lane);
+      continue;  // the same block, the same verdict in every wave
+    }
+    const uint32_t n = (uint32_t)(d.rows * d.cols);
+    const uint8_t* const seg = arc + d.src;
+    const uint8_t* const seg_end = seg + d.size;
+    StreamIn PN;
+    issue_stream(PN, seg, seg_end, n, lane);
+    drain_loads();
+    stage_inputs(S, lane, PN);
+    const uint64_t cnt = reinterpret_cast<const uint64_t*>(S.bcast)[0], nb = reinterpret_cast<const uint64_t*>(S.bcast)[1];
+    const uint32_t lw = reinterpret_cast<const uint32_t*>(S.sorted)[lane];
+    wave_sync();
+    const bool head_ok = cnt == n && cnt <= d.size - 272 && nb / 8 + (nb % 8 != 0) == d.size - 272 - cnt;
+    Book bk{0, 0, false};
+    if (head_ok) bk = build_book(S, lane, lw);
+    const bool split = head_ok && !bk.err && bk.fast && nb >= 64ull * kSerialWaves;  // workgroup-uniform
+    uint32_t errs = 0;
+    if (split) {
+      Stream st;
+      st.lengths = seg + 16;
+      st.sm = seg + 272;
+      st.bits = st.sm + cnt;
+      st.nbits = nb;
+      st.count = n;
+      st.start = 0;
+      const uint64_t b1 = nb * (w + 1) / kSerialWaves;
+      // Round 0 decodes every range from its speculative entry; round v >= 1
+      // proves range v's start (and decodes it again from its predecessor's
+      // exit when it is not that exit).  One decode call site for all rounds.
+      uint64_t from = nb * w / kSerialWaves;
+      bool spec = w > 0, todo = true;
+      for (uint32_t v = 0; v < kSerialWaves; ++v) {
+        if (todo) {
+          ScratchWriter C{mine, cap};
+          Range rg{b1, spec, from, b1, 0u};
+          const uint32_t e = decode_fast(S, lane, st, bk.maxlen, seg_end, C, PN, false, from, 0, &rg);
+          if (lane == 0) {
+            R[w] = SerialPart{rg.first, rg.exit, rg.count, e};
+            if (C.overflow) over = 1;
+          }
+        }
+        __syncthreads();
+        if (v + 1 == kSerialWaves) break;
+        const uint32_t u = v + 1;
+        const uint64_t px = R[v].exit, ub1 = nb * (u + 1) / kSerialWaves;
+        const bool pass = px >= ub1;  // no codeword starts in range u
+        const bool redo = !pass && R[u].first != px;
+        __syncthreads();  // every wave has read R before wave u rewrites it
+        if (w == u && pass && lane == 0) R[u] = SerialPart{px, px, 0u, 0u};
+        todo = w == u && redo;
+        from = px;
+        spec = false;
+      }
+      uint32_t tot = 0, pre = 0;
+      for (uint32_t v = 0; v < kSerialWaves; ++v) {
+        pre += v < w ? R[v].count : 0u;
+        tot += R[v].count;
+        errs |= R[v].err;
+      }
+      if (!errs && (tot != n || R[kSerialWaves - 1].exit != nb)) errs = kErrStream;
+      if (!over && !errs)
+        place_range(mine, st, pre, R[w].count, out + d.dst, d.rows, d.cols, unit_aligned(0, n, d.rows, d.cols),
+                    lane);
+    }
+    if (!split || over) {  // one wave, the single-wave path from the stream's start
+      if (w == 0) {
+        issue_stream(PN, seg, seg_end, n, lane);
+        drain_loads();
+        stage_inputs(S, lane, PN);
+        Writer C{out + d.dst, d.rows, d.cols, (uint32_t)(d.cols / 16), unit_aligned(0, n, d.rows, d.cols)};
+        errs = run_stream(S, lane, seg, seg_end, n, 0, C, NextStream{nullptr, nullptr, 0u}, PN);
+      }
+    }
+    if (w == 0) set_status(status, d.status_slot, errs, lane);
+    __syncthreads();  // R, `over` and the scratch regions are reused by the next block
   }
 }
 
@@ -2182,6 +2410,25 @@ hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t code
     hipLaunchKernelGGL(k_decode_serial, dim3(grid_for(nblocks, per_cu * cus)), blk, 0, s, blocks, nblocks, arc, out,
                        status, queue);
   }
+  return hipGetLastError();
+}
+
+uint64_t serial_wg_scratch(uint32_t nblocks, uint64_t max_elems, unsigned cus, uint32_t* grid, uint32_t* cap) {
+  static const unsigned per_cu = groups_per_cu(k_decode_serial_wg, 64 * kSerialWaves);
+  *grid = grid_for(nblocks, per_cu * cus);
+  // A range holds about max_elems / kSerialWaves symbols; twice that, plus
+  // room for a consume call's last 16-byte store, before it overflows (then
+  // the block is decoded by one wave).
+  const uint64_t c = (2 * ((max_elems + kSerialWaves - 1) / kSerialWaves) + 1024 + 255) & ~255ull;
+  *cap = (uint32_t)c;
+  return (uint64_t)*grid * kSerialWaves * c;
+}
+
+hipError_t launch_decode_serial_wg(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint8_t* out,
+                                   uint32_t* status, uint8_t* scratch, uint32_t cap, uint32_t grid, hipStream_t s) {
+  if (!nblocks) return hipSuccess;
+  hipLaunchKernelGGL(k_decode_serial_wg, dim3(grid), dim3(64 * kSerialWaves), 0, s, blocks, nblocks, arc, out, status,
+                     scratch, cap);
   return hipGetLastError();
 }
 
