@@ -134,5 +134,5 @@ def test_resident_linear_from_archive(hip, path, name, tokens):
     yb = rl(xb).float()  # bf16 in -> bf16 out: one final rounding, relative error <= 2^-8
     want = xb.double() @ wt.T
     assert (torch.linalg.norm(yb.double() - want) / torch.linalg.norm(want)).item() <= 2 ** -8
-    assert torch.equal(rl.decode_weight().view(torch.int16).cpu(), torch.from_numpy(w.view(np.int16)))
+    assert torch.equal(rl.decode_weight().view(torch.int16).cpu(), torch.from_numpy(w.view(np.int16).copy()))
     rl.check_errors()
