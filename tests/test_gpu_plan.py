@@ -118,6 +118,32 @@ def test_plan_reports_corrupt_blocks(hip, oracle):
         assert host[b * 131072:(b + 1) * 131072].tobytes() == raw_bytes(w[16 * b:16 * b + 16])
 
 
+@pytest.mark.parametrize("nblocks", [4, 300, 8192])
+def test_plan_decode_both_schedules(hip, oracle, nblocks):
+    """Parallel32 plans below and above twice the resident waves (6,144 on 256 CUs): the
+    first two run one work item per substream, the last one wave per block.  Plan entry i
+    decodes encoded 16x1024 slab i % 64 into its own output; the entries of the one corrupt
+    slab are the only ones reported and every other entry decodes exactly."""
+    w = syn.normal_bf16(43, (16 * 64, 1024))
+    enc, base = hip.encode_tensor(w, 2, 1024)
+    assert len(base) == 64 and set(base["codec"]) == {2}
+    enc = enc.copy()
+    _corrupt_code_bits(oracle, enc, base[1])
+    table = np.resize(base, nblocks).copy()
+    table["out_offset"] = np.arange(nblocks, dtype=np.uint64) * 32768
+    d_arc = _upload(enc)
+    out = torch.zeros(nblocks * 32768, dtype=torch.uint8, device="cuda")
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    plan.decode(d_arc.data_ptr(), out.data_ptr(), out.numel())
+    n, first, bits = plan.errors()
+    plan.close()
+    bad = np.arange(nblocks) % 64 == 1
+    assert (n, first) == (int(bad.sum()), 1) and bits == xksv_hip.ERR_STREAM
+    host = out.cpu().numpy().reshape(nblocks, -1)
+    want = w.view(np.uint8).reshape(64, -1)[np.arange(nblocks) % 64]
+    assert np.array_equal(host[~bad], want[~bad])
+
+
 @pytest.mark.parametrize("codec", [1, 2])
 @pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336), (100, 4096), (1024, 4100)])
 def test_plan_gemv_whole_tensor(hip, codec, shape):

@@ -2009,12 +2009,13 @@ struct ItemLoc {
   uint32_t count, s0, chunks, err;
   bool run;
 };
-template <class Acc>
-__device__ __forceinline__ ItemLoc locate_item(const DevBlock& d, const uint8_t* blk, uint32_t k, uint64_t hv,
-                                               uint32_t lane) {
+// Substream k of an XKSP2 block from the header words of issue_head: its
+// segment, element count and first tiled position (run = false when the
+// header fails or the block has no substream k).
+__device__ __forceinline__ ItemLoc locate_sub(const DevBlock& d, const uint8_t* blk, uint32_t k, uint64_t hv,
+                                              uint32_t lane) {
   ItemLoc L{nullptr, nullptr, 0u, 0u, 0u, 0u, false};
   L.err = check_head(hv, d.size, d, lane, L.chunks);
-  if (!L.err && (d.rows != 16 || d.cols % 16)) L.err = kErrShape;
   if (L.err || k >= L.chunks) return L;
   const uint64_t len = lane >= 4 && lane < 4 + L.chunks ? hv : 0ull;
   const uint64_t incl = wave_incl(len, lane);
@@ -2025,9 +2026,75 @@ __device__ __forceinline__ ItemLoc locate_item(const DevBlock& d, const uint8_t*
   L.count = rdlane(starts, k + 1) - L.s0;
   L.seg = blk + (end - rdlane64(len, 4 + k));
   L.end = blk + end;
-  if (!Acc::fits(L.s0, L.count, d.rows, d.cols)) L.err = kErrShape;
-  L.run = !L.err;
+  L.run = true;
   return L;
+}
+// As locate_sub, for a fused GEMM item: the slab must be 16 full-tile rows and
+// the substream fit consumer Acc.
+template <class Acc>
+__device__ __forceinline__ ItemLoc locate_item(const DevBlock& d, const uint8_t* blk, uint32_t k, uint64_t hv,
+                                               uint32_t lane) {
+  ItemLoc L = locate_sub(d, blk, k, hv, lane);
+  if (!L.err && (d.rows != 16 || d.cols % 16)) L.err = kErrShape;
+  if (L.err && L.run) L.run = false;
+  if (L.run && !Acc::fits(L.s0, L.count, d.rows, d.cols)) {
+    L.err = kErrShape;
+    L.run = false;
+  }
+  return L;
+}
+
+// Decode XKSP2 blocks by substream (work item i = substream i % 32 of block
+// i / 32; wave w takes items w, w + gridDim.x, ...): for plans with fewer
+// blocks than resident waves, where one wave per block would leave the GPU
+// idle and run each block's substreams one after another.  The next item's
+// inputs and the header of the one after load while an item decodes.
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+k_decode_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_t* __restrict__ arc,
+               uint8_t* __restrict__ out, uint32_t* __restrict__ status) {
+  __shared__ Smem S;
+  const uint32_t lane = lane_id(), stride = gridDim.x;
+  const uint32_t nitems = nblocks * kMaxChunks;
+  uint32_t i = blockIdx.x;
+  if (i >= nitems) return;
+  uint64_t hv = issue_head(arc + blocks[i / kMaxChunks].src, blocks[i / kMaxChunks].size, lane);
+  uint64_t hvn = i + stride < nitems
+                     ? issue_head(arc + blocks[(i + stride) / kMaxChunks].src, blocks[(i + stride) / kMaxChunks].size, lane)
+                     : 0ull;
+  ItemLoc L = locate_sub(blocks[i / kMaxChunks], arc + blocks[i / kMaxChunks].src, i % kMaxChunks, hv, lane);
+  StreamIn PN;
+  if (L.run) {
+    issue_stream(PN, L.seg, L.end, L.count, lane);
+    drain_loads();
+    stage_inputs(S, lane, PN);
+  }
+  for (;;) {
+    const uint32_t in = i + stride, inn = in + stride, k = i % kMaxChunks;
+    const DevBlock d = blocks[i / kMaxChunks];
+    ItemLoc LN{nullptr, nullptr, 0u, 0u, 0u, 0u, false};
+    uint64_t hvnn = 0ull;
+    if (in < nitems) {
+      const DevBlock dn = blocks[in / kMaxChunks];
+      LN = locate_sub(dn, arc + dn.src, in % kMaxChunks, hvn, lane);
+      if (inn < nitems) hvnn = issue_head(arc + blocks[inn / kMaxChunks].src, blocks[inn / kMaxChunks].size, lane);
+    }
+    uint32_t err = L.err;  // a header error is reported by the block's item 0
+    if (L.run) {
+      const bool aligned = d.rows % 16 == 0 && d.cols % 16 == 0 && unit_aligned(L.s0, L.count, d.rows, d.cols);
+      Writer C{out + d.dst, d.rows, d.cols, (uint32_t)(d.cols / 16), aligned};
+      err = run_stream(S, lane, L.seg, L.end, L.count, L.s0, C,
+                       NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN);
+    } else if (LN.run) {
+      issue_stream(PN, LN.seg, LN.end, LN.count, lane);
+      drain_loads();
+      stage_inputs(S, lane, PN);
+    }
+    if (k == 0 || L.run) set_status(status, d.status_slot, err, lane);
+    if (in >= nitems) break;
+    i = in;
+    L = LN;
+    hvn = hvnn;
+  }
 }
 
 // Fused decode-GEMM over XKSP2 blocks of 16-row slabs, one substream per work
@@ -2403,6 +2470,12 @@ hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t code
   const dim3 blk(64);
   if (codec == kCodecParallel) {
     static const unsigned per_cu = groups_per_cu(k_decode_parallel, 64);
+    if ((uint64_t)nblocks < 2ull * per_cu * cus) {  // few blocks: by substream (k_decode_items)
+      static const unsigned per_cu_i = groups_per_cu(k_decode_items, 64);
+      hipLaunchKernelGGL(k_decode_items, dim3(grid_for((uint64_t)nblocks * kMaxChunks, per_cu_i * cus)), blk, 0, s,
+                         blocks, nblocks, arc, out, status);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_decode_parallel, dim3(grid_for(nblocks, per_cu * cus)), blk, 0, s, blocks, nblocks, arc, out,
                        status, queue);
   } else {
