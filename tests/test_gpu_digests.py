@@ -5,7 +5,8 @@ digests of src/compile.cpp:255,443,489 that src/verify.cpp:262-273 checks).
 Pinned against hashlib on: raw blocks of every length class of the padding
 rule (r = n mod 64 below 56, exactly 55/56, 63/64/65, two-chunk padding) at
 aligned and odd output offsets; whole tensors under both codecs; a damaged
-block, whose digest must differ while the others stay exact.
+block, whose digest must differ while the others stay exact; blocks of mixed
+sizes, several to a hashing lane.
 """
 from __future__ import annotations
 
@@ -91,4 +92,30 @@ def test_damaged_block_digest_differs(hip):
     for i, t in enumerate(table):
         o, n = int(t["out_offset"]), int(t["raw_size"])
         assert (got[i] == hashlib.sha256(raw[o:o + n]).digest()) == (i != 2)
+    plan.close()
+
+
+def test_packed_hashing_lanes(hip):
+    """Blocks of mixed sizes in shuffled table order: the largest ones hashed alone, the smaller
+    ones several to a lane (largest first, packed up to 0.6 of the largest); every digest lands
+    in its own block's slot and equals hashlib's."""
+    rng = np.random.default_rng(17)
+    sizes = [458752] * 3 + [131072] * 40 + [65536] * 9 + [8192] * 7 + [1000, 57, 0, 3]
+    rng.shuffle(sizes)
+    table = np.zeros(len(sizes), dtype=RAW)
+    at = 0
+    for i, n in enumerate(sizes):
+        table[i]["offset"] = table[i]["out_offset"] = at
+        table[i]["size"] = table[i]["raw_size"] = n
+        at += n + (-n % 16)  # keep most blocks 16-byte aligned
+    data = rng.integers(0, 256, at, dtype=np.uint8)
+    d_arc = torch.from_numpy(data).to("cuda")
+    out = torch.zeros(at, dtype=torch.uint8, device="cuda")
+    plan = xksv_hip.Plan(hip, table, at)
+    plan.decode(d_arc.data_ptr(), out.data_ptr(), at)
+    assert plan.errors()[0] == 0
+    got = _digests(plan, out, len(sizes))
+    for t, g in zip(table, got):
+        o, n = int(t["out_offset"]), int(t["raw_size"])
+        assert g == hashlib.sha256(data[o:o + n].tobytes()).digest(), n
     plan.close()

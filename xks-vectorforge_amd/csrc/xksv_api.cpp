@@ -283,6 +283,9 @@ struct xksv_hip_plan {
   uint32_t serial_grid = 0, serial_cap = 0;
   uint8_t* item_mem = nullptr;  // ItemScratch of the fused XKSP2 list (none: workgroup-per-block kernels)
   uint8_t* digests = nullptr;   // verification: SHA-256 per block, table order (allocated on first use)
+  HashItem* hash_items = nullptr;  // blocks in hashing order, and the first item of each hashing lane
+  uint32_t* hash_first = nullptr;
+  uint32_t n_hash_lanes = 0;
   uint16_t* index = nullptr;    // codeword index of the fused XKSP2 items (ItemScratch::index)
   uint64_t index_bytes = 0;
   ItemScratch items{};
@@ -291,11 +294,43 @@ struct xksv_hip_plan {
 
 namespace {
 
-bool upload(const std::vector<DevBlock>& v, DevBlock** dst) {
+template <class T>
+bool upload(const std::vector<T>& v, T** dst) {
   *dst = nullptr;
   if (v.empty()) return true;
-  if (hipMalloc(reinterpret_cast<void**>(dst), v.size() * sizeof(DevBlock)) != hipSuccess) return false;
-  return hipMemcpy(*dst, v.data(), v.size() * sizeof(DevBlock), hipMemcpyHostToDevice) == hipSuccess;
+  if (hipMalloc(reinterpret_cast<void**>(dst), v.size() * sizeof(T)) != hipSuccess) return false;
+  return hipMemcpy(*dst, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice) == hipSuccess;
+}
+
+// Hashing schedule for the per-block SHA-256.  One lane hashes a block from
+// start to end, so a launch lasts at least as long as its largest block
+// (a 458 KB slab: 18.1 ms alone), and longer when that lane's wave shares a
+// SIMD with other waves.  Blocks go out largest first, so the lanes of a wave
+// carry about equal work, and a lane takes further blocks (next fit) while its
+// byte total stays within 0.6 of the largest block.  Measured on the Llama-3-8B
+// archive (8,192 slabs of 458 KB, 85,840 of 131 KB): one block per lane
+// 22.6 ms, two 131 KB slabs per lane 21.4 ms (800 waves), three 30.7 ms (576
+// waves, the waves then sharing SIMDs more).
+void hash_schedule(const std::vector<xksv_hip_block>& blocks, std::vector<HashItem>& items,
+                   std::vector<uint32_t>& first) {
+  std::vector<uint32_t> order(blocks.size());
+  for (uint32_t i = 0; i < order.size(); ++i) order[i] = i;
+  std::stable_sort(order.begin(), order.end(),
+                   [&](uint32_t a, uint32_t b) { return blocks[a].raw_size > blocks[b].raw_size; });
+  const uint64_t cap = order.empty() ? 0 : blocks[order[0]].raw_size / 10 * 6;
+  items.clear();
+  first.assign(1, 0);
+  uint64_t load = 0;
+  for (uint32_t i : order) {
+    const uint64_t n = blocks[i].raw_size;
+    if (!items.empty() && load + n > cap) {
+      first.push_back((uint32_t)items.size());
+      load = 0;
+    }
+    items.push_back(HashItem{blocks[i].out_offset, n, i, 0});
+    load += n;
+  }
+  if (!items.empty()) first.push_back((uint32_t)items.size());
 }
 
 // GEMM routing: fused kernels for 16-row compressed slabs whose streams start
@@ -530,6 +565,13 @@ int xksv_hip_plan_create(const xksv_hip_block* blocks, size_t nblocks, uint64_t 
     if (ok) P->out_extent = std::max(P->out_extent, b.out_offset + b.raw_size);
   }
   ok = ok && upload(ser, &P->d_serial) && upload(par, &P->d_parallel) && upload(raw, &P->d_raw);
+  if (ok) {
+    std::vector<HashItem> items;
+    std::vector<uint32_t> first;
+    hash_schedule(P->blocks, items, first);
+    ok = upload(items, &P->hash_items) && upload(first, &P->hash_first);
+    P->n_hash_lanes = (uint32_t)(first.size() - 1);
+  }
   P->n_serial = (uint32_t)ser.size();
   if (ok && !ser.empty()) {  // serial blocks decode a workgroup each
     uint64_t max_elems = 0;
@@ -562,7 +604,7 @@ int xksv_hip_plan_destroy(xksv_hip_plan* P) {
   for (void* p : {(void*)P->d_serial, (void*)P->d_parallel, (void*)P->d_raw, (void*)P->status, (void*)P->g_fserial,
                   (void*)P->g_fparallel, (void*)P->g_gser, (void*)P->g_gpar, (void*)P->g_gplain, (void*)P->g_raw,
                   (void*)P->scratch, (void*)P->item_mem, (void*)P->digests, (void*)P->index,
-                  (void*)P->serial_scratch})
+                  (void*)P->serial_scratch, (void*)P->hash_items, (void*)P->hash_first})
     if (p) (void)hipFree(p);
   if (cur >= 0 && cur != P->device) (void)hipSetDevice(cur);
   delete P;
@@ -660,11 +702,7 @@ int xksv_hip_plan_digests(xksv_hip_plan* P, const void* out, uint64_t out_size, 
   if (!P || !out || !digests || out_size < P->out_extent || digests_size < 32ull * P->blocks.size()) return 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* o = static_cast<const uint8_t*>(out);
-  return launch_sha256_blocks(P->d_serial, P->n_serial, o, digests, s) != hipSuccess ||
-                 launch_sha256_blocks(P->d_parallel, P->n_parallel, o, digests, s) != hipSuccess ||
-                 launch_sha256_blocks(P->d_raw, P->n_raw, o, digests, s) != hipSuccess
-             ? 1
-             : 0;
+  return launch_sha256_lanes(P->hash_items, P->hash_first, P->n_hash_lanes, o, digests, s) == hipSuccess ? 0 : 1;
 }
 
 int xksv_hip_plan_verify(xksv_hip_plan* P, const void* out, uint64_t out_size, const uint8_t* expected,

@@ -87,10 +87,11 @@ hipError_t launch_or_status(const uint32_t* status, uint32_t n, uint32_t* flags,
 // for a header that does not parse (the fused kernels report it).
 hipError_t launch_route_parallel(const DevBlock* blocks, uint32_t n, const uint8_t* arc, uint32_t* flags,
                                  hipStream_t s);
-// SHA-256 of each block's decoded bytes out[dst, dst + raw bytes) into
-// digests[32 * status_slot] (xksv_sha256.hip).
-hipError_t launch_sha256_blocks(const DevBlock* blocks, uint32_t nblocks, const uint8_t* out, uint8_t* digests,
-                                hipStream_t s);
+// SHA-256 of blocks' decoded bytes (xksv_sha256.hip): lane l hashes
+// items[first[l] .. first[l + 1]) one after another, item i's bytes
+// out[dst, dst + n) into digests[32 * slot].
+hipError_t launch_sha256_lanes(const HashItem* items, const uint32_t* first, uint32_t nlanes, const uint8_t* out,
+                               uint8_t* digests, hipStream_t s);
 // verdicts[i] = status[i] | kErrDigest when digests[32 i ..] != expected[32 i ..].
 hipError_t launch_digest_verdicts(const uint8_t* digests, const uint8_t* expected, const uint32_t* status, uint32_t n,
                                   uint32_t* verdicts, hipStream_t s);

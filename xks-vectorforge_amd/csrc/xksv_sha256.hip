@@ -3,13 +3,16 @@
 // every block [src/compile.cpp:255,443,489], which verification compares
 // after decoding [src/verify.cpp:262-273].
 //
-// One lane per block: SHA-256 is sequential within a message, and an archive
-// has tens of thousands of blocks, so lanes hash independent blocks side by
-// side.  The 64 rounds are unrolled with the round constants as immediates;
-// the message schedule is a rolling 16-word window in registers.  A lane
-// reads its block 64 bytes at a time (four 16-byte loads when the block is
-// 16-byte aligned, as every slab of a decoded tensor is; byte loads
-// otherwise).
+// SHA-256 is sequential within a message, so one lane hashes a whole block
+// and lanes hash independent blocks side by side; the time of a launch is
+// that of its longest lane.  The host therefore hands each lane a list of
+// blocks (largest first, smaller ones packed up to 0.6 of the largest block's
+// size), so that the lanes of a wave carry equal work and the waves are
+// fewer.  The 64 rounds are unrolled with the round constants
+// as immediates; the message schedule is a rolling 16-word window in
+// registers.  A lane reads its block 64 bytes at a time (four 16-byte loads
+// when the block is 16-byte aligned, as every slab of a decoded tensor is;
+// byte loads otherwise).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -29,6 +32,15 @@ constexpr uint32_t kSha256K[64] = {
     0x748f82eeu, 0x78a5636fu, 0x84c87814u, 0x8cc70208u, 0x90befffau, 0xa4506cebu, 0xbef9a3f7u, 0xc67178f2u};
 
 __device__ __forceinline__ uint32_t rotr(uint32_t x, uint32_t n) { return __builtin_amdgcn_alignbit(x, x, n); }
+// Three-input bitwise functions in one v_bitop3_b32 each (the immediate is the
+// function's truth table over the inputs 0xf0, 0xcc, 0xaa); both are symmetric
+// in their inputs.  The compiler otherwise splits each three-way XOR into two.
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+__device__ __forceinline__ uint32_t maj3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0xe8);
+}
 __device__ __forceinline__ uint32_t be32(uint32_t v) { return __builtin_amdgcn_perm(0u, v, 0x00010203u); }
 
 // One 64-byte chunk (16 big-endian words) into the state.
@@ -41,16 +53,16 @@ __device__ __forceinline__ void compress(uint32_t (&h)[8], uint32_t (&w)[16]) {
       wt = w[t];
     } else {
       const uint32_t w15 = w[(t - 15) & 15], w2 = w[(t - 2) & 15];
-      const uint32_t s0 = rotr(w15, 7) ^ rotr(w15, 18) ^ (w15 >> 3);
-      const uint32_t s1 = rotr(w2, 17) ^ rotr(w2, 19) ^ (w2 >> 10);
+      const uint32_t s0 = xor3(rotr(w15, 7), rotr(w15, 18), w15 >> 3);
+      const uint32_t s1 = xor3(rotr(w2, 17), rotr(w2, 19), w2 >> 10);
       wt = w[t & 15] + s0 + w[(t - 7) & 15] + s1;
       w[t & 15] = wt;
     }
-    const uint32_t S1 = rotr(e, 6) ^ rotr(e, 11) ^ rotr(e, 25);
+    const uint32_t S1 = xor3(rotr(e, 6), rotr(e, 11), rotr(e, 25));
     const uint32_t ch = (e & f) ^ (~e & g);
     const uint32_t t1 = k + S1 + ch + kSha256K[t] + wt;
-    const uint32_t S0 = rotr(a, 2) ^ rotr(a, 13) ^ rotr(a, 22);
-    const uint32_t mj = (a & b) ^ (a & c) ^ (b & c);
+    const uint32_t S0 = xor3(rotr(a, 2), rotr(a, 13), rotr(a, 22));
+    const uint32_t mj = maj3(a, b, c);
     k = g;
     g = f;
     f = e;
@@ -70,38 +82,50 @@ __device__ __forceinline__ void compress(uint32_t (&h)[8], uint32_t (&w)[16]) {
   h[7] += k;
 }
 
-// Block b's decoded bytes: out[dst, dst + raw bytes); digest into
-// digests[32 * status_slot].
-__global__ void __launch_bounds__(256) k_sha256_blocks(const DevBlock* __restrict__ blocks, uint32_t nblocks,
-                                                       const uint8_t* __restrict__ out, uint8_t* __restrict__ digests) {
-  const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= nblocks) return;
-  const DevBlock d = blocks[b];
-  const uint64_t n = d.codec == kCodecRaw ? d.size : d.rows * d.cols * 2;
-  const uint8_t* p = out + d.dst;
+// The SHA-256 digest of the n bytes at p into digest[0, 32).
+__device__ void sha256(const uint8_t* __restrict__ p, uint64_t n, uint8_t* __restrict__ digest) {
   uint32_t h[8] = {0x6a09e667u, 0xbb67ae85u, 0x3c6ef372u, 0xa54ff53au,
                    0x510e527fu, 0x9b05688cu, 0x1f83d9abu, 0x5be0cd19u};
   uint32_t w[16];
   const uint64_t full = n / 64;
-  const bool aligned = (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
-  for (uint64_t c = 0; c < full; ++c) {
-    const uint8_t* q = p + 64 * c;
-    if (aligned) {
-      const uint4* q4 = reinterpret_cast<const uint4*>(q);
+  if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+    // The next chunk is in flight while this one is compressed (~1,400 VALU
+    // instructions), which hides the memory latency that the one or two
+    // waves per SIMD of this launch cannot (-4 % on the Llama-3-8B archive).  The last chunk reloads itself,
+    // so the load needs no branch (a conditional load would make the
+    // compiler copy the chunk between register sets, waiting on the load).
+    const uint4* q4 = reinterpret_cast<const uint4*>(p);
+    uint4 nxt[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) nxt[i] = full ? q4[i] : make_uint4(0u, 0u, 0u, 0u);
+    for (uint64_t c = 0; c < full; ++c) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint4 v = q4[i];
-        w[4 * i] = be32(v.x);
-        w[4 * i + 1] = be32(v.y);
-        w[4 * i + 2] = be32(v.z);
-        w[4 * i + 3] = be32(v.w);
+        w[4 * i] = be32(nxt[i].x);
+        w[4 * i + 1] = be32(nxt[i].y);
+        w[4 * i + 2] = be32(nxt[i].z);
+        w[4 * i + 3] = be32(nxt[i].w);
       }
-    } else {
+      // The empty asm hides the chunk index from the optimiser, which would
+      // otherwise see that nxt equals a load at the chunk's own address and
+      // re-issue that load where the chunk is used, waiting on it there.
+      uint64_t at = 4 * (c + 1 < full ? c + 1 : c);
+      asm volatile("" : "+v"(at));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) nxt[i] = q4[at + i];
+      // Keep the loads ahead of the compression: the scheduler would sink
+      // them past it (to free their registers), back to where they are used.
+      __builtin_amdgcn_sched_barrier(0);
+      compress(h, w);
+    }
+  } else {
+    for (uint64_t c = 0; c < full; ++c) {
+      const uint8_t* q = p + 64 * c;
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         w[i] = ((uint32_t)q[4 * i] << 24) | ((uint32_t)q[4 * i + 1] << 16) | ((uint32_t)q[4 * i + 2] << 8) | q[4 * i + 3];
+      compress(h, w);
     }
-    compress(h, w);
   }
   // Padding: the r remaining bytes, 0x80, zeros, then the bit length
   // (big-endian 64-bit) in the last 8 bytes; two chunks when r >= 56.
@@ -126,9 +150,21 @@ __global__ void __launch_bounds__(256) k_sha256_blocks(const DevBlock* __restric
     }
     compress(h, w);
   }
-  uint32_t* dg = reinterpret_cast<uint32_t*>(digests + 32ull * d.status_slot);
+  uint32_t* dg = reinterpret_cast<uint32_t*>(digest);
 #pragma unroll
   for (int i = 0; i < 8; ++i) dg[i] = be32(h[i]);
+}
+
+// Lane l hashes items[first[l] .. first[l + 1]) in order.
+__global__ void __launch_bounds__(256) k_sha256_lanes(const HashItem* __restrict__ items,
+                                                      const uint32_t* __restrict__ first, uint32_t nlanes,
+                                                      const uint8_t* __restrict__ out, uint8_t* __restrict__ digests) {
+  const uint32_t l = blockIdx.x * blockDim.x + threadIdx.x;
+  if (l >= nlanes) return;
+  for (uint32_t i = first[l], e = first[l + 1]; i < e; ++i) {
+    const HashItem it = items[i];
+    sha256(out + it.dst, it.n, digests + 32ull * it.slot);
+  }
 }
 
 // Per-block verdict of a verification pass: the block's decode error bits
@@ -163,10 +199,10 @@ hipError_t launch_digest_verdicts(const uint8_t* digests, const uint8_t* expecte
   return hipGetLastError();
 }
 
-hipError_t launch_sha256_blocks(const DevBlock* blocks, uint32_t nblocks, const uint8_t* out, uint8_t* digests,
-                                hipStream_t s) {
-  if (!nblocks) return hipSuccess;
-  hipLaunchKernelGGL(k_sha256_blocks, dim3((nblocks + 255) / 256), dim3(256), 0, s, blocks, nblocks, out, digests);
+hipError_t launch_sha256_lanes(const HashItem* items, const uint32_t* first, uint32_t nlanes, const uint8_t* out,
+                               uint8_t* digests, hipStream_t s) {
+  if (!nlanes) return hipSuccess;
+  hipLaunchKernelGGL(k_sha256_lanes, dim3((nlanes + 255) / 256), dim3(256), 0, s, items, first, nlanes, out, digests);
   return hipGetLastError();
 }
 

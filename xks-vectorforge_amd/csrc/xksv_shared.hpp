@@ -35,6 +35,14 @@ struct DevBlock {
   uint32_t status_slot;  // index into the status array
 };
 
+// One block to hash: its decoded bytes out[dst, dst + n), digest slot.
+struct HashItem {
+  uint64_t dst;
+  uint64_t n;
+  uint32_t slot;
+  uint32_t reserved;
+};
+
 // Device element limit per block: element indices are 32-bit in the kernels.
 constexpr uint64_t kMaxBlockElems = (1ull << 31) - 1;
 // Most substreams an XKSP2 block may hold (src/c_api.cpp:66-72).
