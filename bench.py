@@ -396,6 +396,17 @@ def digest_bench(torch, plan, d_out, raw_total, table, steps, stream):
             "sample_checked": 64, "sample_match_hashlib": bool(ok)}
 
 
+def small_benches(torch, lib, steps, warmup, stream):
+    """The 4096x4096 matrix under the serial codec (20 rotated copies) and the mixed archive
+    under both codecs."""
+    c1 = small_archive_bench(torch, lib, [((4096, 4096), "normal", 0)], 1, steps, warmup, stream, copies=20)
+    mixed = [((4096, 4096), "normal", 1), ((4096, 4096), "student_t", 2), ((4096, 4096), "uniform", 3),
+             ((4096, 4096), "zeros", 4), ((4096,), "fp32", 5)]
+    c3 = {"serial": small_archive_bench(torch, lib, mixed, 1, steps, warmup, stream),
+          "parallel": small_archive_bench(torch, lib, mixed, 2, steps, warmup, stream)}
+    return c1, c3
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -408,7 +419,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemm-copies", type=int, default=4)
     ap.add_argument("--gemm-batches", default="1,4,8,16", help="batches of the 70B-shape GEMM (comma list)")
-    ap.add_argument("--only", choices=["all", "decode", "gemv", "gemm", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "decode", "digests", "gemv", "gemm", "small", "copy"], default="all",
                     help="run one part only (for profiler runs); prints no result line")
     args = ap.parse_args()
     gemm_batches = tuple(int(b) for b in args.gemm_batches.split(","))
@@ -440,6 +451,14 @@ def main() -> int:
     if args.only == "copy":
         log(f"copy {copy_bench(torch, args.steps, stream):.1f} GB/s (2 GiB read + 2 GiB written per step)")
         return 0
+    if args.only == "small":
+        c1, c3 = small_benches(torch, lib, args.steps, args.warmup, stream)
+        log(f"4096x4096 serial {c1['ms']} ms ({c1['decoded_gbps']} GB/s, exact {c1['bit_exact']}); mixed serial "
+            f"{c3['serial']['ms']} ms / parallel {c3['parallel']['ms']} ms")
+        abi = abi_bench(torch, lib)
+        log("host-pointer ABI per block: " + ", ".join(f"{k} {v['parallel32']['ms_median']} / {v['serial']['ms_median']} ms"
+                                                       for k, v in abi.items() if isinstance(v, dict) and "serial" in v))
+        return 0
 
     d_arc, table, meta, raw_total, encs = build_archive(torch, lib, args.layers, 2)
     d_out = torch.empty(raw_total, dtype=torch.uint8, device="cuda")
@@ -466,6 +485,8 @@ def main() -> int:
     dg = digest_bench(torch, plan, d_out, raw_total, table, args.steps, stream)
     log(f"slab SHA-256 on the GPU: {dg['ms']} ms for {dg['blocks']} blocks ({dg['decoded_gbps_hashed']} GB/s), "
         f"sample matches hashlib: {dg['sample_match_hashlib']}")
+    if args.only == "digests":
+        return 0
 
     g1 = gemv_bench(torch, lib, 14336, 4096, args.gemv_copies, args.steps, args.warmup, stream)
     g2 = gemv_bench(torch, lib, 4096, 14336, args.gemv_copies, args.steps, args.warmup, stream)
@@ -474,11 +495,7 @@ def main() -> int:
                                       stream) for r, c in ((28672, 8192), (8192, 28672))}
     log("gemm bf16 " + "; ".join(f"{k}: " + ", ".join(f"b{b} {v['us_per_layer']} us" for b, v in g["batches"].items())
                                  for k, g in g5.items()))
-    c1 = small_archive_bench(torch, lib, [((4096, 4096), "normal", 0)], 1, args.steps, args.warmup, stream, copies=20)
-    mixed = [((4096, 4096), "normal", 1), ((4096, 4096), "student_t", 2), ((4096, 4096), "uniform", 3),
-             ((4096, 4096), "zeros", 4), ((4096,), "fp32", 5)]
-    c3 = {"serial": small_archive_bench(torch, lib, mixed, 1, args.steps, args.warmup, stream),
-          "parallel": small_archive_bench(torch, lib, mixed, 2, args.steps, args.warmup, stream)}
+    c1, c3 = small_benches(torch, lib, args.steps, args.warmup, stream)
     log(f"4096x4096 serial {c1['decoded_gbps']} GB/s exact={c1['bit_exact']}; mixed serial "
         f"{c3['serial']['decoded_gbps']} / parallel {c3['parallel']['decoded_gbps']} GB/s")
     copy_gbps = copy_bench(torch, 10, stream)
