@@ -122,13 +122,16 @@ def test_plan_reports_corrupt_blocks(hip, oracle):
 def test_plan_decode_both_schedules(hip, oracle, nblocks):
     """Parallel32 plans below and above twice the resident waves (6,144 on 256 CUs): the
     first two run one work item per substream, the last one wave per block.  Plan entry i
-    decodes encoded 16x1024 slab i % 64 into its own output; the entries of the one corrupt
-    slab are the only ones reported and every other entry decodes exactly."""
+    decodes encoded 16x1024 slab i % 64 into its own output; the entries of the two corrupt
+    slabs (code bits of slab 1, header magic of slab 2) are the only ones reported and every
+    other entry decodes exactly."""
     w = syn.normal_bf16(43, (16 * 64, 1024))
     enc, base = hip.encode_tensor(w, 2, 1024)
     assert len(base) == 64 and set(base["codec"]) == {2}
     enc = enc.copy()
     _corrupt_code_bits(oracle, enc, base[1])
+    enc[int(base[2]["offset"])] ^= 0x01  # magic
+    assert oracle.unpack_parallel(enc[int(base[2]["offset"]):int(base[2]["offset"] + base[2]["size"])].tobytes())[0] != 0
     table = np.resize(base, nblocks).copy()
     table["out_offset"] = np.arange(nblocks, dtype=np.uint64) * 32768
     d_arc = _upload(enc)
@@ -137,8 +140,8 @@ def test_plan_decode_both_schedules(hip, oracle, nblocks):
     plan.decode(d_arc.data_ptr(), out.data_ptr(), out.numel())
     n, first, bits = plan.errors()
     plan.close()
-    bad = np.arange(nblocks) % 64 == 1
-    assert (n, first) == (int(bad.sum()), 1) and bits == xksv_hip.ERR_STREAM
+    bad = np.isin(np.arange(nblocks) % 64, (1, 2))
+    assert (n, first) == (int(bad.sum()), 1) and bits == xksv_hip.ERR_STREAM | xksv_hip.ERR_HEADER
     host = out.cpu().numpy().reshape(nblocks, -1)
     want = w.view(np.uint8).reshape(64, -1)[np.arange(nblocks) % 64]
     assert np.array_equal(host[~bad], want[~bad])
