@@ -1373,6 +1373,7 @@ struct GemmArgs {
 template <int NB>
 struct GemmF32 {
   static constexpr int kCols = NB, kOut = 16 * NB;
+  static constexpr bool kDirect = false;  // partial sums go through LDS slots (deposit)
   const float* x;
   uint64_t ldx;
   uint32_t nb;
@@ -1482,6 +1483,7 @@ struct GemmF32 {
 template <int NB>
 struct GemmBf16 {
   static constexpr int kCols = NB, kOut = 16 * NB;
+  static constexpr bool kDirect = false;
   static constexpr uint32_t kXRow = 18;  // staged 16-byte pieces per x row: 9 tiles
   static constexpr uint32_t kXCopies = NB <= 8 ? (kXRow * NB + 63) / 64 : 0;
   const uint16_t* x;
@@ -1588,6 +1590,7 @@ struct GemmMfma {
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   static constexpr int kCols = 16, kOut = 256;
+  static constexpr bool kDirect = true;  // each output is in exactly one lane: records straight from acc
   const uint16_t* x;
   uint64_t ldx;
   uint32_t nb;
@@ -1657,6 +1660,17 @@ struct GemmMfma {
     slots[(r0 + 1) * 16 + n] += acc[1];
     slots[(r0 + 2) * 16 + n] += acc[2];
     slots[(r0 + 3) * 16 + n] += acc[3];
+  }
+  // An item's record, packed as the slots path packs it (row r, column n < nb
+  // at r * nb + n): lane l holds rows 4 (l / 16) .. + 3 of column l % 16.
+  __device__ __forceinline__ void record(float* part, uint32_t nb, uint32_t lane) const {
+    const uint32_t r0 = 4u * (lane >> 4), n = lane & 15u;
+    if (n < nb) {
+      part[(r0 + 0) * nb + n] = acc[0];
+      part[(r0 + 1) * nb + n] = acc[1];
+      part[(r0 + 2) * nb + n] = acc[2];
+      part[(r0 + 3) * nb + n] = acc[3];
+    }
   }
 };
 
@@ -2145,16 +2159,20 @@ k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_
       const uint16_t* idx = is.index ? is.index + (uint64_t)i * is.index_segs * 64 : nullptr;
       err = run_stream(S, lane, L.seg, L.end, L.count, L.s0, C,
                        NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN, idx);
-      float* slots = reinterpret_cast<float*>(S.syms);
-      for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) slots[o] = 0.f;
-      wave_sync();
-      C.deposit(slots, lane, L.s0);
-      wave_sync();
       // Live batch columns only, packed: row r, column j < nb at r * nb + j.
       float* part = is.partial + (uint64_t)i * kMaxItemOut;
-      for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave)
-        if (o % Acc::kCols < ga.nb) part[(o / Acc::kCols) * ga.nb + o % Acc::kCols] = slots[o];
-      wave_sync();
+      if constexpr (Acc::kDirect) {
+        C.record(part, ga.nb, lane);
+      } else {
+        float* slots = reinterpret_cast<float*>(S.syms);
+        for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) slots[o] = 0.f;
+        wave_sync();
+        C.deposit(slots, lane, L.s0);
+        wave_sync();
+        for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave)
+          if (o % Acc::kCols < ga.nb) part[(o / Acc::kCols) * ga.nb + o % Acc::kCols] = slots[o];
+        wave_sync();
+      }
     } else if (LN.run) {
       issue_stream(PN, LN.seg, LN.end, LN.count, lane);
       drain_loads();
