@@ -1373,7 +1373,6 @@ struct GemmArgs {
 template <int NB>
 struct GemmF32 {
   static constexpr int kCols = NB, kOut = 16 * NB;
-  static constexpr bool kDirect = false;  // partial sums go through LDS slots (deposit)
   const float* x;
   uint64_t ldx;
   uint32_t nb;
@@ -1472,6 +1471,23 @@ struct GemmF32 {
 #pragma unroll
       for (int j = 0; j < NB; ++j) slots[row * NB + j] += acc[j];
   }
+  // An item's record (row r, column j < nb at r * nb + j): after the
+  // exchanges of deposit, the one lane of each row that deposits stores it;
+  // those 16 lanes cover the 16 rows once.
+  __device__ __forceinline__ void record(float* part, uint32_t nb, uint32_t lane, uint32_t s0) {
+    const uint32_t su = (s0 >> 3) & 1u;
+    const int partner = (int)((((lane + su) ^ 1u) - su) & 63u);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      acc[j] += __shfl(acc[j], partner, kWave);
+      acc[j] += __shfl_xor(acc[j], 32, kWave);
+    }
+    const uint32_t row = (((s0 >> 3) + lane) >> 1) & 15u;
+    if (lane < 32 && ((lane + su) & 1u) == 0)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        if (j < (int)nb) part[row * nb + j] = acc[j];
+  }
 };
 
 // bf16 activations in the layout of x @ W.T: X[j * ldx + c] (batch rows),
@@ -1483,7 +1499,6 @@ struct GemmF32 {
 template <int NB>
 struct GemmBf16 {
   static constexpr int kCols = NB, kOut = 16 * NB;
-  static constexpr bool kDirect = false;
   static constexpr uint32_t kXRow = 18;  // staged 16-byte pieces per x row: 9 tiles
   static constexpr uint32_t kXCopies = NB <= 8 ? (kXRow * NB + 63) / 64 : 0;
   const uint16_t* x;
@@ -1576,6 +1591,23 @@ struct GemmBf16 {
 #pragma unroll
       for (int j = 0; j < NB; ++j) slots[row * NB + j] += acc[j];
   }
+  // An item's record (row r, column j < nb at r * nb + j): after the
+  // exchanges of deposit, the one lane of each row that deposits stores it;
+  // those 16 lanes cover the 16 rows once.
+  __device__ __forceinline__ void record(float* part, uint32_t nb, uint32_t lane, uint32_t s0) {
+    const uint32_t su = (s0 >> 3) & 1u;
+    const int partner = (int)((((lane + su) ^ 1u) - su) & 63u);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      acc[j] += __shfl(acc[j], partner, kWave);
+      acc[j] += __shfl_xor(acc[j], 32, kWave);
+    }
+    const uint32_t row = (((s0 >> 3) + lane) >> 1) & 15u;
+    if (lane < 32 && ((lane + su) & 1u) == 0)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        if (j < (int)nb) part[row * nb + j] = acc[j];
+  }
 };
 
 // bf16 activations (layout of GemmBf16), bf16 MFMA with fp32 accumulation
@@ -1590,7 +1622,6 @@ struct GemmMfma {
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   static constexpr int kCols = 16, kOut = 256;
-  static constexpr bool kDirect = true;  // each output is in exactly one lane: records straight from acc
   const uint16_t* x;
   uint64_t ldx;
   uint32_t nb;
@@ -1663,7 +1694,7 @@ struct GemmMfma {
   }
   // An item's record, packed as the slots path packs it (row r, column n < nb
   // at r * nb + n): lane l holds rows 4 (l / 16) .. + 3 of column l % 16.
-  __device__ __forceinline__ void record(float* part, uint32_t nb, uint32_t lane) const {
+  __device__ __forceinline__ void record(float* part, uint32_t nb, uint32_t lane, uint32_t) const {
     const uint32_t r0 = 4u * (lane >> 4), n = lane & 15u;
     if (n < nb) {
       part[(r0 + 0) * nb + n] = acc[0];
@@ -2159,20 +2190,9 @@ k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_
       const uint16_t* idx = is.index ? is.index + (uint64_t)i * is.index_segs * 64 : nullptr;
       err = run_stream(S, lane, L.seg, L.end, L.count, L.s0, C,
                        NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN, idx);
-      // Live batch columns only, packed: row r, column j < nb at r * nb + j.
-      float* part = is.partial + (uint64_t)i * kMaxItemOut;
-      if constexpr (Acc::kDirect) {
-        C.record(part, ga.nb, lane);
-      } else {
-        float* slots = reinterpret_cast<float*>(S.syms);
-        for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave) slots[o] = 0.f;
-        wave_sync();
-        C.deposit(slots, lane, L.s0);
-        wave_sync();
-        for (uint32_t o = lane; o < (uint32_t)Acc::kOut; o += kWave)
-          if (o % Acc::kCols < ga.nb) part[(o / Acc::kCols) * ga.nb + o % Acc::kCols] = slots[o];
-        wave_sync();
-      }
+      // Live batch columns only, packed: row r, column j < nb at r * nb + j;
+      // every output of the item sits in one lane, which stores it.
+      C.record(is.partial + (uint64_t)i * kMaxItemOut, ga.nb, lane, L.s0);
     } else if (LN.run) {
       issue_stream(PN, LN.seg, LN.end, LN.count, lane);
       drain_loads();
