@@ -65,7 +65,7 @@ def test_gemm_bf16_rejects_bad_input(hip):
 
 
 @pytest.mark.parametrize("rows,cols,codec", [(512, 8192, 2), (64, 28672, 2), (256, 4096, 1), (40, 4096, 2)])
-@pytest.mark.parametrize("batch", [1, 8, 16])
+@pytest.mark.parametrize("batch", [1, 4, 8, 16])
 def test_plan_gemm_bf16(hip, rows, cols, codec, batch):
     """Whole tensors at the Llama-3-70B slab widths (8192, 28672) through the plan.
 
@@ -84,6 +84,30 @@ def test_plan_gemm_bf16(hip, rows, cols, codec, batch):
     plan.gemm_bf16(arc.data_ptr(), x.data_ptr(), batch, y.data_ptr())
     assert plan.errors() == (0, -1, 0)
     want = (x.double() @ wt.double().T).cpu().numpy()
+    err = _rel_l2(y.cpu().numpy(), want)
+    assert err <= TOL_BF16 and err <= TOL_TIGHT, err
+    plan.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(28672, 8192), (8192, 28672)])
+def test_plan_gemm_bf16_70b_full_shapes(hip, rows, cols):
+    """The Llama-3-70B MLP matrices at full size, N(0, 0.02) weights, batch 4 through the
+    plan (MFMA consumer, codeword index), against fp64."""
+    batch = 4
+    g = torch.Generator(device="cuda")
+    g.manual_seed(rows // 16 + cols)
+    wt = (torch.randn(rows, cols, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    words = wt.view(torch.int16).cpu().numpy().view(np.uint16)
+    enc, table = hip.encode_tensor(words, 2)
+    table["out_offset"] //= cols * 2
+    arc = torch.from_numpy(enc).to("cuda")
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    x = _x_bf16(batch, cols, 7)
+    y = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
+    plan.gemm_bf16(arc.data_ptr(), x.data_ptr(), batch, y.data_ptr())
+    assert plan.errors() == (0, -1, 0)
+    want = (x.double() @ wt.double().T).cpu().numpy()
+    del wt
     err = _rel_l2(y.cpu().numpy(), want)
     assert err <= TOL_BF16 and err <= TOL_TIGHT, err
     plan.close()
