@@ -1471,9 +1471,9 @@ struct GemmF32 {
 #pragma unroll
       for (int j = 0; j < NB; ++j) slots[row * NB + j] += acc[j];
   }
-  // An item's record (row r, column j < nb at r * nb + j): after the
-  // exchanges of deposit, the one lane of each row that deposits stores it;
-  // those 16 lanes cover the 16 rows once.
+  // An item's record (row r, column j < nb at r * nb + j): the same two
+  // exchanges as deposit, then the one lane per row that deposit would use
+  // stores the row's sums; those 16 lanes cover the 16 rows once.
   __device__ __forceinline__ void record(float* part, uint32_t nb, uint32_t lane, uint32_t s0) {
     const uint32_t su = (s0 >> 3) & 1u;
     const int partner = (int)((((lane + su) ^ 1u) - su) & 63u);
@@ -1591,9 +1591,9 @@ struct GemmBf16 {
 #pragma unroll
       for (int j = 0; j < NB; ++j) slots[row * NB + j] += acc[j];
   }
-  // An item's record (row r, column j < nb at r * nb + j): after the
-  // exchanges of deposit, the one lane of each row that deposits stores it;
-  // those 16 lanes cover the 16 rows once.
+  // An item's record (row r, column j < nb at r * nb + j): the same two
+  // exchanges as deposit, then the one lane per row that deposit would use
+  // stores the row's sums; those 16 lanes cover the 16 rows once.
   __device__ __forceinline__ void record(float* part, uint32_t nb, uint32_t lane, uint32_t s0) {
     const uint32_t su = (s0 >> 3) & 1u;
     const int partner = (int)((((lane + su) ^ 1u) - su) & 63u);
