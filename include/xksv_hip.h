@@ -146,6 +146,18 @@ int xksv_hip_plan_destroy(xksv_hip_plan* plan);
  * collected per block, read them with xksv_hip_plan_errors. */
 int xksv_hip_plan_decode(xksv_hip_plan* plan, const void* archive, void* out, uint64_t out_size, void* stream);
 
+/* No reference counterpart (a load-time sidecar for weights that stay
+ * resident and are decoded again and again, the GPU-resident path of
+ * python/runtime.py:86-99,248-287): build, on `stream`, a codeword index of
+ * the plan's parallel32 blocks from `archive` -- the bit offset of every 32nd
+ * codeword of every substream, 128 bytes per 2,048 symbols (~4 % of the
+ * encoded size) -- which later xksv_hip_plan_decode calls use to start each
+ * lane of a wave at a known codeword.  Every entry is checked as it is used,
+ * so an index built from another archive only costs speed: a substream whose
+ * entries do not chain is decoded without them, with identical results and
+ * errors.  A second call rebuilds it.  0 on success, 1 on error. */
+int xksv_hip_plan_index(xksv_hip_plan* plan, const void* archive, void* stream);
+
 /* Enqueue fused decode-GEMM, fp32 X [cols, batch] row-major, Y [rows, batch]
  * (block rows start at out_offset).  All blocks must share `cols`; raw blocks
  * (rows = cols = 0 in archive indexes) take it from the compressed ones, and a

@@ -288,6 +288,9 @@ struct xksv_hip_plan {
   uint32_t n_hash_lanes = 0;
   uint16_t* index = nullptr;    // codeword index of the fused XKSP2 items (ItemScratch::index)
   uint64_t index_bytes = 0;
+  uint16_t* dindex = nullptr;   // decode index of d_parallel (xksv_hip_plan_index), per-block offsets dibase
+  uint64_t* dibase = nullptr;
+  uint64_t dindex_bytes = 0;
   ItemScratch items{};
   std::vector<uint32_t> h_status;
 };
@@ -603,7 +606,8 @@ int xksv_hip_plan_destroy(xksv_hip_plan* P) {
   if (P->device >= 0 && cur != P->device) (void)hipSetDevice(P->device);
   for (void* p : {(void*)P->d_serial, (void*)P->d_parallel, (void*)P->d_raw, (void*)P->status, (void*)P->g_fserial,
                   (void*)P->g_fparallel, (void*)P->g_gser, (void*)P->g_gpar, (void*)P->g_gplain, (void*)P->g_raw,
-                  (void*)P->scratch, (void*)P->item_mem, (void*)P->digests, (void*)P->index,
+                  (void*)P->scratch, (void*)P->item_mem, (void*)P->digests, (void*)P->index, (void*)P->dindex,
+                  (void*)P->dibase,
                   (void*)P->serial_scratch, (void*)P->hash_items, (void*)P->hash_first})
     if (p) (void)hipFree(p);
   if (cur >= 0 && cur != P->device) (void)hipSetDevice(cur);
@@ -620,14 +624,43 @@ int xksv_hip_plan_decode(xksv_hip_plan* P, const void* archive, void* out, uint6
   uint8_t* o = static_cast<uint8_t*>(out);
   uint32_t* queue = P->status + P->blocks.size();
   if (launch_fill_u32(P->status, P->blocks.size() + kQueues, 0, s) != hipSuccess) return 1;
-  if (launch_decode(P->d_parallel, P->n_parallel, kCodecParallel, arc, o, P->status, queue, (unsigned)di->cus, s) !=
-      hipSuccess)
+  if (launch_decode(P->d_parallel, P->n_parallel, kCodecParallel, arc, o, P->status, queue, (unsigned)di->cus, s,
+                    P->dindex, P->dibase) != hipSuccess)
     return 1;
   if (launch_decode_serial_wg(P->d_serial, P->n_serial, arc, o, P->status, P->serial_scratch, P->serial_cap,
                               P->serial_grid, s) != hipSuccess)
     return 1;
   if (launch_copy_raw(P->d_raw, P->n_raw, arc, o, s) != hipSuccess) return 1;
   return 0;
+}
+
+int xksv_hip_plan_index(xksv_hip_plan* P, const void* archive, void* stream) {
+  if (!P || (!archive && P->archive_size)) return 1;
+  if (!current_device(nullptr)) return 1;
+  if (!P->n_parallel) return 0;
+  if (!P->dindex) {
+    // Block b's items get segs_b segments of kIdxSegSyms symbols, enough for
+    // the 32 substreams the slab rule writes; other items stay unindexed.
+    std::vector<DevBlock> par(P->n_parallel);
+    if (hipMemcpy(par.data(), P->d_parallel, par.size() * sizeof(DevBlock), hipMemcpyDeviceToHost) != hipSuccess)
+      return 1;
+    std::vector<uint64_t> base(par.size() + 1, 0);
+    for (size_t i = 0; i < par.size(); ++i) {
+      const uint64_t syms = (par[i].rows * par[i].cols + kMaxChunks - 1) / kMaxChunks;
+      const uint64_t segs = std::max<uint64_t>(1, (syms + kIdxSegSyms - 1) / kIdxSegSyms);
+      base[i + 1] = base[i] + segs * kMaxChunks * 64;
+    }
+    P->dindex_bytes = base.back() * sizeof(uint16_t);
+    if (!upload(base, &P->dibase)) return 1;
+    if (hipMalloc(reinterpret_cast<void**>(&P->dindex), P->dindex_bytes) != hipSuccess) {
+      P->dindex = nullptr;
+      return 1;
+    }
+  }
+  return launch_index_items(P->d_parallel, P->n_parallel, static_cast<const uint8_t*>(archive), P->dindex, 0,
+                            static_cast<hipStream_t>(stream), P->dibase) == hipSuccess
+             ? 0
+             : 1;
 }
 
 // The plan GEMMs: fused kernels over 16-row compressed slabs, decode to

@@ -52,8 +52,11 @@ int run_block_at(uint8_t* base, const BlockLayout& L, const uint8_t* input, uint
 // Kernel launchers (xksv_kernels.hip).  `cus` = the device's CU count; each
 // launcher sizes its persistent grid to the workgroups resident at once.
 // `queue` (optional) is a zeroed counter the decode waves claim blocks from.
+// `index`, `ibase` (optional, XKSP2): a codeword index of `blocks` laid out by
+// launch_index_items with `ibase`; the decode checks it as it uses it.
 hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc, uint8_t* out,
-                         uint32_t* status, uint32_t* queue, unsigned cus, hipStream_t s);
+                         uint32_t* status, uint32_t* queue, unsigned cus, hipStream_t s,
+                         const uint16_t* index = nullptr, const uint64_t* ibase = nullptr);
 // Serial blocks decoded by a workgroup each (k_decode_serial_wg): scratch
 // bytes for `nblocks` blocks of at most `max_elems` elements; sets the grid
 // and the per-wave region size the launch takes.
@@ -79,9 +82,11 @@ hipError_t launch_gemm_plain_bf16(const DevBlock* blocks, uint32_t nblocks, cons
                                   uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t s);
 // Codeword index (ItemScratch::index) of the fused XKSP2 items of `blocks`:
-// `segs` segments of 64 u16 entries per item.
+// `segs` segments of 64 u16 entries per item; with `ibase` (nblocks + 1
+// entry offsets), block b's items take (ibase[b + 1] - ibase[b]) / 2048
+// entries each from ibase[b] on instead.
 hipError_t launch_index_items(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint16_t* index,
-                              uint32_t segs, hipStream_t s);
+                              uint32_t segs, hipStream_t s, const uint64_t* ibase = nullptr);
 // *flags |= OR of status[0 .. n) (vector atomic), enqueued on s.
 hipError_t launch_or_status(const uint32_t* status, uint32_t n, uint32_t* flags, hipStream_t s);
 // flags[i] for XKSP2 block i: bit 0 = substreams on 8-element boundaries

@@ -128,6 +128,12 @@ static_assert(kIdxStride % 8 == 4, "indexed lane slots: odd dword stride");
 constexpr uint32_t kXOff = kWave * kIdxStride;
 constexpr uint32_t kXBytes = 4096;
 static_assert(kXOff + kXBytes <= kSymsBytes, "staged X must fit the symbol buffer");
+// Index segments (64 u16 entries each) copied to LDS ahead of their use, two
+// buffers (segment sg in buffer sg % 2): past the staged X and the tables'
+// scratch, so the first lands while the tables are built.
+constexpr uint32_t kIxOff = kXOff + kXBytes;
+static_assert(kIxOff + 256 <= kSymsBytes && kIxOff >= kLut1Off + 4 * (1u << kLutBits) && kIxOff % 16 == 0,
+              "index entries must fit the symbol buffer beside the tables' scratch");
 
 // ------------------------------------------------------------------ helpers
 
@@ -1112,6 +1118,10 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
 // continues the stream speculatively from there (decode_fast), which decodes
 // it -- or reports its error -- exactly as decode does.  Otherwise it returns
 // true with the stream's error bits in `err`.
+//
+// The entries are read from LDS (kIxOff): segment 0's are copied there by
+// the caller while the tables are built, each later segment's one segment
+// ahead, so no segment waits on them.
 template <class Cons, bool kL3 = false>
 __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen,
                                                const uint8_t* blk_end, Cons& C, const StreamIn& PN, bool next,
@@ -1126,7 +1136,7 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
   cur.v = make_uint4(0u, 0u, 0u, 0u);
   cur.drop = 16;
   for (uint32_t sg = 0; pos0 < st.count; ++sg) {
-    const uint16_t* e = idx + 64 * sg;
+    const uint16_t* e = reinterpret_cast<const uint16_t*>(S.syms + kIxOff + 128 * (sg & 1));
     const uint32_t span = e[0];
     const uint32_t rel = lane ? e[lane] : 0u;
     const uint32_t rel_next = lane < 63 ? e[lane + 1] : span;
@@ -1149,6 +1159,10 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
     const uint64_t nextbit = segbit + span;
     const bool more = pos0 + n_s < st.count;
     if (more && lane < kStreamLanes) cur = fetch16(st.bits + (nextbit >> 3) + 16 * lane, bend);
+    // the next segment's entries (inside the item's allotment: the caller
+    // passes an index only for streams it holds whole); landed by the drain
+    // before this segment's consume
+    if (more && lane < 8) copy_to_lds16(idx + 64 * (sg + 1) + 8 * lane, S.syms + kIxOff + 128 * ((sg + 1) & 1));
     SmWin W;
     issue_sm<kIdxSegSyms / 8 / kWave>(W, st.sm, pos0, st.count, Cons::lane_unit(lane));
     C.stage_x(S, lane, st, pos0, n_s);  // lands in LDS during the walk
@@ -1319,6 +1333,10 @@ __device__ __forceinline__ uint32_t stream_body(Smem& S, uint32_t lane, const ui
   wave_sync();  // the staged inputs are read before the tables overwrite them
   N.issue(PN, lane);
   if (cnt != count || cnt > len - 272 || nb / 8 + (nb % 8 != 0) != len - 272 - cnt) return fail_stream(S, lane, kErrHeader, N, PN);
+  // The index's first segment lands in LDS while the tables are built (no
+  // register held across the build); every path below waits for it before
+  // the symbol buffer is written past the tables' scratch.
+  if (idx && lane < 8) copy_to_lds16(idx + 8 * lane, S.syms + kIxOff);
   Stream st;
   st.lengths = seg + 16;
   st.sm = seg + 272;
@@ -1327,11 +1345,12 @@ __device__ __forceinline__ uint32_t stream_body(Smem& S, uint32_t lane, const ui
   st.count = count;
   st.start = start;
   const Book b = build_book<kL3>(S, lane, lw);
+  if (idx) drain_loads();
   if (b.err) return fail_stream(S, lane, b.err, N, PN);
   if (!b.fast) return decode_slow(S, lane, st, C, PN, N.seg);
   uint64_t rbit = 0;
   uint32_t rpos = 0, err = 0;
-  if (idx && idx[0] != kIdxNone &&
+  if (idx && reinterpret_cast<const uint16_t*>(S.syms + kIxOff)[0] != kIdxNone &&
       decode_indexed<Cons, kL3>(S, lane, st, b.maxlen, seg_end, C, PN, N.seg, idx, err, rbit, rpos))
     return err;
   return decode_fast<Cons, kL3>(S, lane, st, b.maxlen, seg_end, C, PN, N.seg, rbit, rpos);
@@ -1368,23 +1387,23 @@ struct Writer {
   bool xs = false;  // no activations
   __device__ __forceinline__ void stage_x(Smem&, uint32_t, const Stream&, uint32_t, uint32_t) {}
   static __device__ __forceinline__ uint32_t lane_unit(uint32_t lane) { return lane; }
+  template <bool kIx>
   __device__ __forceinline__ void unit(const Smem& S, const Stream& st, uint32_t pos0, uint32_t u, uint64_t M) const {
-    uint64_t E;
-    __builtin_memcpy(&E, S.syms + 8 * u, 8);
-    const uint4 w = combine8(E, M);
+    const uint4 w = combine8(unit_exps<kIx>(S.syms, u), M);
     const uint32_t U = ((st.start + pos0) >> 3) + u, T = U >> 5;
     const uint32_t band = rows == 16 ? 0u : T / tpb;
     const uint32_t row = 16u * band + ((U >> 1) & 15u);
     const uint32_t col = 16u * (T - band * tpb) + 8u * (U & 1u);
     __builtin_memcpy(out + 2ull * (row * (uint32_t)cols + col), &w, 16);
   }
-  template <bool kIx = false>  // never fed by the indexed walk
+  // kIx: the symbols are in the indexed walk's lane slots.
+  template <bool kIx = false>
   __device__ __forceinline__ uint32_t consume(Smem& S, uint32_t lane, const Stream& st, uint32_t pos0, uint32_t avail, bool final,
                               const SmWin& W) {
     if (!aligned) {
       for (uint32_t i = lane; i < avail; i += kWave) {
         const uint32_t P = pos0 + i;
-        const uint32_t e = S.syms[i], s = st.sm[P];
+        const uint32_t e = S.syms[kIx ? kIdxStride * (i / kIdxLaneSyms) + i % kIdxLaneSyms : i], s = st.sm[P];
         const uint16_t w = (uint16_t)(((s & 0x80u) << 8) | (e << 7) | (s & 0x7fu));
         uint32_t row, col;
         tile_to_rc(st.start + P, (uint32_t)rows, (uint32_t)cols, row, col);
@@ -1402,9 +1421,7 @@ struct Writer {
 #pragma unroll
       for (uint32_t i = 0; i < kSmWin; ++i) {
         if (lane + kWave * i < units) {
-          uint64_t E;
-          __builtin_memcpy(&E, S.syms + 8 * (lane + kWave * i), 8);
-          const uint4 w = combine8(E, W.v[i]);
+          const uint4 w = combine8(unit_exps<kIx>(S.syms, lane + kWave * i), W.v[i]);
           __builtin_memcpy(p + 64 * i, &w, 16);
         }
       }
@@ -1412,11 +1429,11 @@ struct Writer {
 #pragma unroll
       for (uint32_t i = 0; i < kSmWin; ++i) {
         const uint32_t u = lane + kWave * i;
-        if (u < units) unit(S, st, pos0, u, W.v[i]);
+        if (u < units) unit<kIx>(S, st, pos0, u, W.v[i]);
       }
     }
     for (uint32_t u = lane + kSmWin * kWave; u < units; u += kWave)
-      unit(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
+      unit<kIx>(S, st, pos0, u, ldg64(st.sm + pos0 + 8 * u));
     return take;
   }
 };
@@ -1896,13 +1913,29 @@ __device__ __forceinline__ uint32_t claim_next(uint32_t* queue, uint32_t b, uint
   return gridDim.x + rdlane(t, 0);
 }
 
+// Substream k's codeword index within a per-block index (launch_index_items
+// with `ibase`), or nullptr: none given, or more symbols than the block's
+// allotment holds (the indexed walk then never reads past the allotment).
+__device__ __forceinline__ const uint16_t* stream_index(const uint16_t* index, const uint64_t* ibase, uint32_t b,
+                                                        uint32_t k, uint32_t count) {
+  if (!index) return nullptr;
+  const uint64_t o0 = ibase[b];
+  const uint32_t segs = (uint32_t)((ibase[b + 1] - o0) / (64u * kMaxChunks));
+  return count <= segs * kIdxSegSyms ? index + o0 + (uint64_t)k * segs * 64 : nullptr;
+}
+
 // Decode XKSP2 blocks: one wave per block, its substreams in order, each
 // substream's inputs prefetched while the previous one decodes; the next
 // block's header is prefetched at the start of each block.
+// kIdx: with a codeword index (a separate instantiation, so that the decode
+// without one compiles as if the indexed walk did not exist).
+template <bool kIdx>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
 k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
                                                         const uint8_t* __restrict__ arc, uint8_t* __restrict__ out,
-                                                        uint32_t* __restrict__ status, uint32_t* queue) {
+                                                        uint32_t* __restrict__ status, uint32_t* queue,
+                                                        const uint16_t* __restrict__ index,
+                                                        const uint64_t* __restrict__ ibase) {
   __shared__ Smem S;
   const uint32_t lane = lane_id();
   uint32_t b = blockIdx.x;
@@ -1936,7 +1969,8 @@ k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
       const uint32_t ncount = k + 1 < chunks ? rdlane(starts, k + 2) - s1 : 0u;
       C.aligned = aligned && unit_aligned(s0, s1 - s0, d.rows, d.cols);
       err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, C,
-                       NextStream{k + 1 < chunks ? blk + noff : nullptr, blk + noff + nlen, ncount}, PN);
+                       NextStream{k + 1 < chunks ? blk + noff : nullptr, blk + noff + nlen, ncount}, PN,
+                       kIdx ? stream_index(index, ibase, b, k, s1 - s0) : nullptr);
       off = noff;
       len = nlen;
     }
@@ -2228,9 +2262,11 @@ __device__ __forceinline__ ItemLoc locate_item(const DevBlock& d, const uint8_t*
 // blocks than resident waves, where one wave per block would leave the GPU
 // idle and run each block's substreams one after another.  The next item's
 // inputs and the header of the one after load while an item decodes.
+template <bool kIdx>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
 k_decode_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_t* __restrict__ arc,
-               uint8_t* __restrict__ out, uint32_t* __restrict__ status) {
+               uint8_t* __restrict__ out, uint32_t* __restrict__ status, const uint16_t* __restrict__ index,
+               const uint64_t* __restrict__ ibase) {
   __shared__ Smem S;
   const uint32_t lane = lane_id(), stride = gridDim.x;
   const uint32_t nitems = nblocks * kMaxChunks;
@@ -2262,7 +2298,8 @@ k_decode_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint
       const bool aligned = d.rows % 16 == 0 && d.cols % 16 == 0 && unit_aligned(L.s0, L.count, d.rows, d.cols);
       Writer C{out + d.dst, d.rows, d.cols, (uint32_t)(d.cols / 16), aligned};
       err = run_stream(S, lane, L.seg, L.end, L.count, L.s0, C,
-                       NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN);
+                       NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN,
+                       kIdx ? stream_index(index, ibase, i / kMaxChunks, k, L.count) : nullptr);
     } else if (LN.run) {
       issue_stream(PN, LN.seg, LN.end, LN.count, lane);
       drain_loads();
@@ -2321,7 +2358,9 @@ k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_
     if (L.run) {
       Acc C(ga);
       C.init();
-      const uint16_t* idx = is.index ? is.index + (uint64_t)i * is.index_segs * 64 : nullptr;
+      // (an item with more symbols than its allotment holds has no index entry)
+      const uint16_t* idx =
+          is.index && L.count <= is.index_segs * kIdxSegSyms ? is.index + (uint64_t)i * is.index_segs * 64 : nullptr;
       err = run_stream<Acc, kL3>(S, lane, L.seg, L.end, L.count, L.s0, C,
                                  NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN, idx);
       // Live batch columns only, packed: row r, column j < nb at r * nb + j;
@@ -2399,16 +2438,20 @@ __device__ __forceinline__ uint64_t load_be64(const uint8_t* p, const uint8_t* e
 struct IdxLane {
   uint64_t lim[34];
 };
+// `ibase` (optional, nblocks + 1 entries): block b's index starts at entry
+// ibase[b] and holds (ibase[b + 1] - ibase[b]) / (64 kMaxChunks) segments per
+// item; without it every item holds `segs` segments, item i at i * segs * 64.
 __global__ void __launch_bounds__(64) k_index_items(const DevBlock* __restrict__ blocks, uint32_t nblocks,
                                                     const uint8_t* __restrict__ arc, uint16_t* __restrict__ index,
-                                                    uint32_t segs) {
+                                                    uint32_t segs, const uint64_t* __restrict__ ibase) {
   __shared__ IdxLane Lanes[64];
   uint64_t* lim = Lanes[threadIdx.x].lim;
   const uint32_t nitems = nblocks * kMaxChunks;
   for (uint32_t i = blockIdx.x * 64 + threadIdx.x; i < nitems; i += gridDim.x * 64) {
-    uint16_t* out = index + (uint64_t)i * segs * 64;
     const DevBlock d = blocks[i / kMaxChunks];
     const uint32_t k = i % kMaxChunks;
+    if (ibase) segs = (uint32_t)((ibase[i / kMaxChunks + 1] - ibase[i / kMaxChunks]) / (64u * kMaxChunks));
+    uint16_t* out = ibase ? index + ibase[i / kMaxChunks] + (uint64_t)k * segs * 64 : index + (uint64_t)i * segs * 64;
     const uint8_t* blk = arc + d.src;
     bool ok = false;
     if (d.size >= 32) {
@@ -2490,7 +2533,7 @@ __global__ void __launch_bounds__(64) k_index_items(const DevBlock* __restrict__
         }
       }
     }
-    if (!ok) out[0] = kIdxNone;
+    if (!ok && segs) out[0] = kIdxNone;
   }
 }
 
@@ -2637,19 +2680,28 @@ static unsigned groups_per_cu(K kernel, unsigned threads) {
 }
 
 hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc, uint8_t* out,
-                         uint32_t* status, uint32_t* queue, unsigned cus, hipStream_t s) {
+                         uint32_t* status, uint32_t* queue, unsigned cus, hipStream_t s, const uint16_t* index,
+                         const uint64_t* ibase) {
   if (!nblocks) return hipSuccess;
   const dim3 blk(64);
   if (codec == kCodecParallel) {
-    static const unsigned per_cu = groups_per_cu(k_decode_parallel, 64);
+    static const unsigned per_cu = groups_per_cu(k_decode_parallel<false>, 64);
     if ((uint64_t)nblocks < 2ull * per_cu * cus) {  // few blocks: by substream (k_decode_items)
-      static const unsigned per_cu_i = groups_per_cu(k_decode_items, 64);
-      hipLaunchKernelGGL(k_decode_items, dim3(grid_for((uint64_t)nblocks * kMaxChunks, per_cu_i * cus)), blk, 0, s,
-                         blocks, nblocks, arc, out, status);
+      static const unsigned per_cu_i = groups_per_cu(k_decode_items<false>, 64);
+      const dim3 grid(grid_for((uint64_t)nblocks * kMaxChunks, per_cu_i * cus));
+      if (index)
+        hipLaunchKernelGGL(k_decode_items<true>, grid, blk, 0, s, blocks, nblocks, arc, out, status, index, ibase);
+      else
+        hipLaunchKernelGGL(k_decode_items<false>, grid, blk, 0, s, blocks, nblocks, arc, out, status, index, ibase);
       return hipGetLastError();
     }
-    hipLaunchKernelGGL(k_decode_parallel, dim3(grid_for(nblocks, per_cu * cus)), blk, 0, s, blocks, nblocks, arc, out,
-                       status, queue);
+    const dim3 grid(grid_for(nblocks, per_cu * cus));
+    if (index)
+      hipLaunchKernelGGL(k_decode_parallel<true>, grid, blk, 0, s, blocks, nblocks, arc, out, status, queue, index,
+                         ibase);
+    else
+      hipLaunchKernelGGL(k_decode_parallel<false>, grid, blk, 0, s, blocks, nblocks, arc, out, status, queue, index,
+                         ibase);
   } else {
     static const unsigned per_cu = groups_per_cu(k_decode_serial, 64);
     hipLaunchKernelGGL(k_decode_serial, dim3(grid_for(nblocks, per_cu * cus)), blk, 0, s, blocks, nblocks, arc, out,
@@ -2783,12 +2835,12 @@ hipError_t launch_or_status(const uint32_t* status, uint32_t n, uint32_t* flags,
 }
 
 hipError_t launch_index_items(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint16_t* index,
-                              uint32_t segs, hipStream_t s) {
+                              uint32_t segs, hipStream_t s, const uint64_t* ibase) {
   if (!nblocks) return hipSuccess;
   const uint64_t items = (uint64_t)nblocks * kMaxChunks;
   const uint64_t g = (items + 63) / 64;
   hipLaunchKernelGGL(k_index_items, dim3(g < 4096 ? (unsigned)g : 4096u), dim3(64), 0, s, blocks, nblocks, arc, index,
-                     segs);
+                     segs, ibase);
   return hipGetLastError();
 }
 

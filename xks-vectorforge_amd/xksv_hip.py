@@ -62,6 +62,7 @@ _SIGNATURES = {
     "xksv_hip_plan_create": (_int, [ctypes.POINTER(Block), _sz, _u64, _pvp]),
     "xksv_hip_plan_destroy": (_int, [_vp]),
     "xksv_hip_plan_decode": (_int, [_vp, _vp, _vp, _u64, _vp]),
+    "xksv_hip_plan_index": (_int, [_vp, _vp, _vp]),
     "xksv_hip_plan_gemm": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "xksv_hip_plan_gemm_bf16": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "xksv_hip_plan_errors": (ctypes.c_int64, [_vp, _vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(_u32)]),
@@ -210,6 +211,12 @@ class Plan:
     def decode(self, archive_ptr: int, out_ptr: int, out_size: int, stream: int = 0) -> None:
         if self.lib.lib.xksv_hip_plan_decode(self.handle, archive_ptr, out_ptr, out_size, stream or None):
             raise XksvError("xksv_hip_plan_decode failed to launch")
+
+    def index(self, archive_ptr: int, stream: int = 0) -> None:
+        """Build the decode's codeword index of the plan's parallel32 blocks from the
+        archive (once, for weights that stay resident); later decodes use it."""
+        if self.lib.lib.xksv_hip_plan_index(self.handle, archive_ptr, stream or None):
+            raise XksvError("xksv_hip_plan_index failed")
 
     def gemm(self, archive_ptr: int, x_ptr: int, batch: int, y_ptr: int, stream: int = 0) -> None:
         if self.lib.lib.xksv_hip_plan_gemm(self.handle, archive_ptr, x_ptr, batch, y_ptr, stream or None):
