@@ -10,10 +10,14 @@ init).  7,504,924,672 elements, 15.0 GB of BF16.  One step = one decode of
 every block of the archive (resident in HBM) into BF16 in HBM, through the
 device-resident plan API of libxksv_hip.so.
 
-`value` = decoded BF16 GB/s (rows*cols*2 bytes per step / step time).
+`value` = decoded BF16 GB/s (rows*cols*2 bytes per step / step time), the
+decode of an archive as it arrives (no sidecar).
 Also reported: roofline fraction of the decode launch (encoded bytes read +
 BF16 bytes written, per launch, over the launch time measured with HIP
-events), the fused batch-1 decode-GEMV time per layer at 14336x4096 and
+events), the same decode after the plan has built its codeword index once
+(a load-time sidecar for weights that stay resident; its build time, its
+bytes and their share of each decode's reads are reported with it), the
+fused batch-1 decode-GEMV time per layer at 14336x4096 and
 4096x14336 (rotating over 16 resident copies so the 256 MB last-level cache
 cannot serve repeats), a plain device copy's GB/s, and the reference CPU
 decode (the reference's own codec compiled from source, oracle/_ref) timed on
@@ -132,6 +136,36 @@ def time_samples(torch, fn, samples: int, per_sample: int, stream) -> dict:
     ms = np.array([a.elapsed_time(b) / per_sample for a, b in evs])
     return {"median": float(np.median(ms)), "p10": float(np.percentile(ms, 10)), "p90": float(np.percentile(ms, 90)),
             "mean": float(ms.mean()), "samples": samples, "calls_per_sample": per_sample}
+
+
+def indexed_decode_bench(torch, plan, d_arc, d_out, raw_total: int, meta, table, alg_bytes: int, steps: int,
+                         stream) -> dict:
+    """The same plan after xksv_hip_plan_index: a codeword index of every parallel32 substream
+    (a load-time sidecar for resident weights, built once and timed here), after which every
+    decode starts each lane of a wave at a recorded codeword.  Its algorithmic bytes add the
+    index entries each decode reads (128 B per 2,048 symbols of a substream)."""
+    s = stream.cuda_stream
+    torch.cuda.synchronize()
+    t0 = time.time()
+    plan.index(d_arc.data_ptr(), s)
+    torch.cuda.synchronize()
+    build_ms = (time.time() - t0) * 1e3
+    d_out.zero_()
+    step = lambda: plan.decode(d_arc.data_ptr(), d_out.data_ptr(), raw_total, s)  # noqa: E731
+    step()
+    nbad = plan.errors(s)[0]
+    ok = nbad == 0 and verify(torch, d_out, meta)
+    t = time_samples(torch, step, steps, 1, stream)
+    par = table[table["codec"] == 2]
+    syms = (par["rows"].astype(np.int64) * par["cols"].astype(np.int64) + 31) // 32
+    index_bytes = int((32 * np.maximum(1, (syms + 2047) // 2048) * 128).sum())
+    alg = alg_bytes + index_bytes
+    ms = t["median"]
+    return {"ms": {k: round(v, 4) for k, v in t.items() if k in ("median", "p10", "p90", "mean")},
+            "decoded_gbps": round(raw_total / (ms * 1e-3) / 1e9, 1), "index_bytes": index_bytes,
+            "index_build_ms": round(build_ms, 1), "algorithmic_bytes_per_launch": alg,
+            "roofline_frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "bit_exact_full_size": bool(ok and plan.errors(s)[0] == 0), "kernel": "k_decode_parallel<true>"}
 
 
 def gemv_bench(torch, lib, rows: int, cols: int, copies: int, steps: int, warmup: int, stream) -> dict:
@@ -419,7 +453,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemm-copies", type=int, default=4)
     ap.add_argument("--gemm-batches", default="1,4,8,16", help="batches of the 70B-shape GEMM (comma list)")
-    ap.add_argument("--only", choices=["all", "decode", "digests", "gemv", "gemm", "small", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "decode", "decode_indexed", "digests", "gemv", "gemm", "small", "copy"], default="all",
                     help="run one part only (for profiler runs); prints no result line")
     args = ap.parse_args()
     gemm_batches = tuple(int(b) for b in args.gemm_batches.split(","))
@@ -482,6 +516,12 @@ def main() -> int:
     log(f"decode {ms:.3f} ms/step, {decoded_gbps:.1f} GB/s decoded, {achieved:.1f} GB/s algorithmic")
     if args.only == "decode":
         return 0
+    dix = indexed_decode_bench(torch, plan, d_arc, d_out, raw_total, meta, table, alg_bytes, args.steps, stream)
+    log(f"decode with the codeword index {dix['ms']['median']} ms/step, {dix['decoded_gbps']} GB/s decoded, "
+        f"roofline {dix['roofline_frac']}, exact={dix['bit_exact_full_size']} (index {dix['index_bytes'] / 1e6:.0f} MB, "
+        f"built once in {dix['index_build_ms']} ms)")
+    if args.only == "decode_indexed":
+        return 0
     dg = digest_bench(torch, plan, d_out, raw_total, table, args.steps, stream)
     log(f"slab SHA-256 on the GPU: {dg['ms']} ms for {dg['blocks']} blocks ({dg['decoded_gbps_hashed']} GB/s), "
         f"sample matches hashlib: {dg['sample_match_hashlib']}")
@@ -526,6 +566,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "bit_exact_full_size": bool(verified and nbad2 == 0),
         "decode_ms": {k: round(v, 4) for k, v in tdec.items() if k in ("median", "p10", "p90", "mean")},
+        "decode_indexed": dix,
         "host_pointer_abi": abi,
         "hbm_pct_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "gemv_us_per_layer_14336x4096": g1["us_per_layer"],
