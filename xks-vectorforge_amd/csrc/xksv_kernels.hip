@@ -1171,9 +1171,9 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
     uint32_t p = base + rel, n = 0, d = 0, wi, w0, w1, w2;
     load_window(S, p, wi, w0, w1, w2);
     lds_bytes const o = as_lds(S.syms + kIdxStride * lane);
-    // A symbol the lane does not want (past its k) is stored into the lane's
-    // own junk byte past its symbols (the slot's padding), so the step has
-    // no branch around the store.
+    // In the three-symbol tail, a symbol the lane does not want (past its k)
+    // is stored into the lane's own junk byte past its symbols (the slot's
+    // padding), so the step has no branch around the store.
     lds_bytes const junk = o + kIdxLaneSyms;
     // One exit condition: a lane walks exactly k symbols.  A path on wrong
     // offsets (a stale index) advances at most 127 bits per step for at most
@@ -1204,22 +1204,20 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
         n += take;
       }
     } else {
-      while (n < k) {
-        const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
-        uint32_t en = S.t.f.lut2[win >> (32 - kLutBits)];
-        if (__builtin_expect(__ballot(en == kLongMark) != 0, 0)) {
-          if (en == kLongMark) {
-            const uint32_t lc = long_code(S, win, maxlen);
-            d |= lc == 0;
-            en = lc ? lc : kDeadMark;
-          }
-        }
-        const uint32_t pair = (en >> 15) & 1u, two = pair & (n + 1 < k ? 1u : 0u);
+      // Steps that cannot pass k store both bytes (a lone symbol's second
+      // byte is rewritten by the next step); a last single symbol takes one
+      // more step that keeps only the entry's first code.
+      while (n + 2 <= k) {
+        const uint32_t en = step2(S, p, wi, w0, w1, w2, maxlen, d);
         o[n] = (uint8_t)en;
-        (two ? o + n + 1 : junk)[0] = (uint8_t)(en >> 16);
-        p += pair & ~two ? (en >> 24) & 15u : (en >> 8) & 127u;
-        n += 1 + two;
-        slide(S, p, wi, w0, w1, w2);
+        o[n + 1] = (uint8_t)(en >> 16);
+        n += 1 + ((en >> 15) & 1u);
+      }
+      if (n < k) {
+        const uint32_t en = step2(S, p, wi, w0, w1, w2, maxlen, d);
+        o[n] = (uint8_t)en;
+        if ((en >> 15) & 1u) p -= ((en >> 8) & 127u) - ((en >> 24) & 15u);
+        n += 1;
       }
     }
     if (__ballot(k && (d || p != limit))) {
