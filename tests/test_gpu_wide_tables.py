@@ -1,6 +1,6 @@
-"""Three-symbol decode tables: fused GEMV/GEMM at batch 1 over slabs of 8,192+ columns (GPU only).
+"""Three-symbol decode tables: fused GEMV/GEMM at batch 1 over slabs of 16,384+ columns (GPU only).
 
-Slabs that wide have substreams of 4,096+ symbols, and the fused batch-1 consumers
+Slabs that wide have substreams of 8,192+ symbols, and the fused batch-1 consumers
 (fp32 x and bf16 x) decode them with the engine's three-symbol table kind: up to three
 codes per 10-bit lookup, codes of 11-32 bits resolved inside the step, codes longer
 than 32 bits on the bit-serial path.  Narrower slabs and every other consumer keep the
@@ -35,7 +35,7 @@ from oracle_lib import craft_segment, raw_bytes
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
-COLS = 8192  # the narrowest slab width that takes the three-symbol tables
+COLS = 16384  # the narrowest slab width that takes the three-symbol tables
 
 
 def _rel_l2(got, want):

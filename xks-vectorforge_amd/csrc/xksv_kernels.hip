@@ -75,8 +75,8 @@ constexpr uint32_t kIdxMaxSpan = kStreamLanes * 128 - 7 - 96 - kLongLen - 32;
 // it, at most three.  kLongEntry (no symbols) marks a window whose first code
 // is longer than 10 bits or matches no code.  Per lookup it takes ~2.9
 // symbols instead of ~2, for a third table read per entry when built: a net
-// gain from ~4,096 symbols per stream (the fused GEMV/GEMM at batch 1 selects
-// it for slabs of 8,192 columns or more).
+// gain on long streams (the fused GEMV/GEMM at batch 1 selects it for slabs
+// of 16,384 columns or more, substreams of 8,192+ symbols).
 constexpr uint32_t kLongEntry = 0;
 struct FastTables {
   union {
@@ -2759,9 +2759,10 @@ static void gemm_any(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, ui
 }
 
 // `wide`: slabs of kL3Cols columns or more, whose substreams are long enough
-// for the three-symbol tables to pay (batch 1; measured: 4096 x 14336 GEMV
-// -4 %, 8192 x 28672 bf16 GEMM -8 %; at 4,096 columns they cost +6 %).
-constexpr uint64_t kL3Cols = 8192;
+// for the three-symbol tables to pay (batch 1; measured against the
+// two-symbol walk: 8192 x 28672 bf16 GEMM -3.5 %; at 14,336 columns even, at
+// 8,192 +6 %, at 4,096 +6 %).
+constexpr uint64_t kL3Cols = 16384;
 template <template <int> class Acc>
 static void gemm_valu(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                       const GemmArgs& ga, uint32_t* status, const ItemScratch* is, unsigned cus, bool wide) {
