@@ -216,7 +216,7 @@ def gemv_bench(torch, lib, rows: int, cols: int, copies: int, steps: int, warmup
 
 
 def gemm_bf16_bench(torch, lib, rows: int, cols: int, batches, copies: int, steps: int, warmup: int, stream) -> dict:
-    """Fused decode-GEMM with bf16 X [batch, cols] (bf16 MFMA from batch 2) over `copies` resident
+    """Fused decode-GEMM with bf16 X [batch, cols] (bf16 MFMA on whole-tile substreams) over `copies` resident
     copies of one parallel32 layer; rel-L2 against an fp64 GEMM of the same bf16 values."""
     import xksv_hip
     w = gen_bf16(torch, (rows, cols), 91 + rows, False)
@@ -250,7 +250,7 @@ def gemm_bf16_bench(torch, lib, rows: int, cols: int, batches, copies: int, step
         out[str(batch)] = {"us_per_layer": round(ms * 1e3, 2), "us_p10": round(t["p10"] * 1e3, 2),
                            "us_p90": round(t["p90"] * 1e3, 2), "gbps": round(alg / (ms * 1e-3) / 1e9, 1),
                            "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "rel_l2_vs_fp64": rel,
-                           "mfma": batch >= 2, "errors": int(nbad)}
+                           "mfma": True, "errors": int(nbad)}
         del ref
     plan.close()
     return {"encoded_bytes": int(enc.nbytes), "copies": copies, "batches": out}

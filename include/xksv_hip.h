@@ -84,8 +84,8 @@ int xksv_hip_gemm_parallel(const void* input, size_t n, size_t batch, const floa
 /* No reference counterpart (the reference's GEMM takes fp32 X only): fused
  * decode-GEMM over an XKSP2 block with bf16 activations in the layout of
  * torch's x @ W.T -- X [batch, cols] bf16 row-major, output [batch, rows] fp32
- * row-major -- accumulated in fp32.  From batch 2, when every substream covers
- * whole 16x16 tiles, the products run on bf16 MFMA (v_mfma_f32_16x16x32_bf16);
+ * row-major -- accumulated in fp32.  When every substream covers whole 16x16
+ * tiles, the products run on bf16 MFMA (v_mfma_f32_16x16x32_bf16);
  * otherwise on the VALU (v_dot2 of bf16 pairs into fp32). */
 int xksv_hip_gemm_parallel_bf16(const void* input, size_t n, size_t batch, const uint16_t* x, float* output);
 
@@ -168,7 +168,7 @@ int xksv_hip_plan_gemm(xksv_hip_plan* plan, const void* archive, const float* x,
 
 /* As xksv_hip_plan_gemm with bf16 activations X [batch, cols] row-major and
  * fp32 output Y [batch, M] row-major, M = the plan's row extent (largest
- * out_offset + rows); bf16 MFMA from batch 2 (see xksv_hip_gemm_parallel_bf16). */
+ * out_offset + rows); bf16 MFMA on whole-tile substreams (see xksv_hip_gemm_parallel_bf16). */
 int xksv_hip_plan_gemm_bf16(xksv_hip_plan* plan, const void* archive, const uint16_t* x, size_t batch, float* y,
                             void* stream);
 

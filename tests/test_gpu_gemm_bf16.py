@@ -1,8 +1,8 @@
 """Fused decode-GEMM with bf16 activations (GPU only).
 
 The layout is that of x @ W.T: X [batch, cols] bf16 row-major, Y [batch, rows]
-fp32 row-major. The products use bf16 MFMA (v_mfma_f32_16x16x32_bf16) from
-batch 2 when every substream covers whole 16x16 tiles; otherwise they use fp32
+fp32 row-major. The products use bf16 MFMA (v_mfma_f32_16x16x32_bf16) at every
+batch when every substream covers whole 16x16 tiles; otherwise they use fp32
 VALU FMAs. The check is the oracle's CPU decode followed by an fp64 GEMM
 against the exact bf16 values of X. Tolerance: relative L2 error <= 2e-3 for
 bf16 activations (the bf16-X bound of the path's parity contract), and every
@@ -35,7 +35,7 @@ def _x_bf16(batch, cols, seed):
     return torch.randn(batch, cols, generator=g, device="cuda").to(torch.bfloat16).contiguous()
 
 
-# 16x4096 and 16x8192: substreams of whole tiles (MFMA from batch 2);
+# 16x4096 and 16x8192: substreams of whole tiles (MFMA at every batch);
 # 16x4112: unit-aligned but not tile-aligned (VALU at every batch);
 # 7x19 and 5x4096: not 16-row slabs (decode to scratch + plain GEMM).
 @pytest.mark.parametrize("rows,cols", [(16, 4096), (16, 8192), (16, 4112), (7, 19), (5, 4096)])

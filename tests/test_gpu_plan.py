@@ -226,7 +226,7 @@ def _resplit(hip, oracle, w, chunks) -> bytes:
 def test_plan_gemm_nonstandard_chunk_counts(hip, oracle, batch):
     """Plan GEMMs over XKSP2 blocks re-split into 32, 5, 7, 1, 31 and 16 substreams: blocks
     whose substreams do not start on 8-element boundaries are routed to decode + plain GEMM,
-    the others to the fused kernels; fp32 X and bf16 X (MFMA from batch 2) both match fp64."""
+    the others to the fused kernels; fp32 X and bf16 X (MFMA on whole-tile substreams) both match fp64."""
     cols = 1024
     counts = (32, 5, 7, 1, 31, 16)
     w = syn.normal_bf16(900 + batch, (16 * len(counts), cols))
@@ -262,7 +262,7 @@ def test_plan_gemm_nonstandard_chunk_counts(hip, oracle, batch):
 def test_plan_gemm_staged_x(hip, batch, cols):
     """Indexed fused GEMMs copy each segment's x columns into LDS when x and its rows are
     16-byte aligned, and read x from global memory otherwise (x shifted by one element).
-    4096 columns: substreams of whole tiles (bf16 MFMA from batch 2, 8-tile segments);
+    4096 columns: substreams of whole tiles (bf16 MFMA, 8-tile segments);
     4112: substreams start mid-tile (VALU consumers, 9-tile segments).  Both layouts, both
     activation types, both placements match fp64; runs at one placement are bit-identical
     to each other."""

@@ -21,7 +21,7 @@ std::vector<SlabSpec> slab_rule(uint64_t nbytes, bool bf16, uint64_t shape_cols)
 // What a block-level call computes.  kDecode: BF16 into `out` (device).
 // kGemmF32: fused GEMM with fp32 X [cols, batch] into Y [rows, batch].
 // kGemmBf16: fused GEMM with bf16 X [batch, cols] into fp32 Y [batch, rows]
-// (bf16 MFMA from batch 2 when every substream covers whole tiles).
+// (bf16 MFMA when every substream covers whole tiles).
 enum Mode { kDecode, kGemmF32, kGemmBf16 };
 struct Fused {
   bool unit = false;  // every stream unit-aligned: fused consumers apply
@@ -69,7 +69,7 @@ hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t co
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
                            const ItemScratch* is, unsigned cus, uint64_t cols, hipStream_t s);
 // bf16 X [batch rows of ldx], Y [batch rows of ldy]; bf16 MFMA when `mfma`
-// (every substream covers whole 16x16 tiles) and nb >= 2, VALU otherwise.
+// (every substream covers whole 16x16 tiles), VALU otherwise.
 // With `is` (scratch of kItemScratchPerBlock bytes per block, see
 // ItemScratch), XKSP2 blocks run by substream over every resident wave.
 hipError_t launch_gemm_bf16(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,

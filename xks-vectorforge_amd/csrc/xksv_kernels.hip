@@ -1760,7 +1760,7 @@ struct GemmBf16 {
 };
 
 // bf16 activations (layout of GemmBf16), bf16 MFMA with fp32 accumulation
-// (batch 2..16, padded to 16): v_mfma_f32_16x16x32_bf16 multiplies a 16 x 32
+// (batch 1..16, padded to 16): v_mfma_f32_16x16x32_bf16 multiplies a 16 x 32
 // slice of W (two 16x16 tiles side by side) by a 32 x 16 slice of X.  Lane
 // l = r + 16 g supplies W row r, columns 8g..8g+7 of the slice -- exactly one
 // decoded unit (half a tile row, unit 32 (g / 2) + 2 r + g % 2 of the tile
@@ -2790,7 +2790,8 @@ hipError_t launch_gemm_bf16(const DevBlock* blocks, uint32_t nblocks, uint32_t c
                             uint32_t* status, const ItemScratch* is, unsigned cus, uint64_t cols, hipStream_t s) {
   if (!nblocks) return hipSuccess;
   const GemmArgs ga{x, ldx, nb, y, ldy};
-  if (mfma && nb >= 2) gemm_any<GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
+  // MFMA at every batch (batch 1 padded: 2-3 % faster than the VALU consumer at the 70B shapes)
+  if (mfma) gemm_any<GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   else gemm_valu<GemmBf16>(s, blocks, nblocks, codec, arc, ga, status, is, cus, cols >= kL3Cols);
   return hipGetLastError();
 }
