@@ -567,6 +567,12 @@ int xksv_hip_plan_create(const xksv_hip_block* blocks, size_t nblocks, uint64_t 
     }
     if (ok) P->out_extent = std::max(P->out_extent, b.out_offset + b.raw_size);
   }
+  // Waves claim parallel32 blocks in list order, so the largest go first: a
+  // block is one wave's work, and a large one claimed last would keep a few
+  // waves busy after the rest have drained (the 16x14336 slabs of a model's
+  // last layer take ~3.5x a 16x4096 slab).  Status slots keep table order.
+  std::stable_sort(par.begin(), par.end(),
+                   [](const DevBlock& a, const DevBlock& b) { return a.rows * a.cols > b.rows * b.cols; });
   ok = ok && upload(ser, &P->d_serial) && upload(par, &P->d_parallel) && upload(raw, &P->d_raw);
   if (ok) {
     std::vector<HashItem> items;
