@@ -147,6 +147,50 @@ def test_plan_decode_both_schedules(hip, oracle, nblocks):
     assert np.array_equal(host[~bad], want[~bad])
 
 
+def test_plan_decode_mixed_sizes_report_table_slots(hip, oracle):
+    """The plan decodes its parallel32 blocks largest first; errors still name table
+    entries.  Table: 16x4096 and 16x14336 slabs interleaved (the 14336-wide ones run
+    first), then a 5x4096 slab; entries 3 (4096-wide) and 4 (14336-wide) carry damaged
+    code bits, entry 6 a damaged magic.  Errors are reported for exactly those entries,
+    the first as 3, and every other entry decodes exactly, with and without the index."""
+    parts, rows_out, want = [], [], []
+    for i in range(8):
+        rows, cols = (16, 14336) if i % 2 else (16, 4096)
+        if i == 7:
+            rows, cols = 5, 4096
+        w = syn.normal_bf16(2000 + i, (rows, cols))
+        parts.append(np.frombuffer(hip.call("xksv_pack_parallel", raw_bytes(w), rows, cols), np.uint8))
+        rows_out.append((rows, cols))
+        want.append(raw_bytes(w))
+    table = np.zeros(len(parts), xksv_hip.BLOCK_DTYPE)
+    off = out = 0
+    for i, (p, (rows, cols)) in enumerate(zip(parts, rows_out)):
+        table[i] = (off, p.nbytes, rows * cols * 2, out, rows, cols, xksv_hip.CODEC_PARALLEL, 0)
+        off += p.nbytes
+        out += rows * cols * 2
+    enc = np.concatenate(parts).copy()
+    _corrupt_code_bits(oracle, enc, table[3])
+    _corrupt_code_bits(oracle, enc, table[4])
+    enc[int(table[6]["offset"])] ^= 0x01
+    d_arc = _upload(enc)
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    try:
+        for indexed in (False, True):
+            if indexed:
+                plan.index(_upload(np.concatenate(parts)).data_ptr())  # from the clean archive
+            o = torch.zeros(out, dtype=torch.uint8, device="cuda")
+            plan.decode(d_arc.data_ptr(), o.data_ptr(), o.numel())
+            n, first, bits = plan.errors()
+            assert (n, first) == (3, 3) and bits == xksv_hip.ERR_STREAM | xksv_hip.ERR_HEADER, indexed
+            host = o.cpu().numpy().tobytes()
+            for i in range(len(parts)):
+                if i not in (3, 4, 6):
+                    a = int(table[i]["out_offset"])
+                    assert host[a:a + len(want[i])] == want[i], (indexed, i)
+    finally:
+        plan.close()
+
+
 @pytest.mark.parametrize("codec", [1, 2])
 @pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336), (100, 4096), (1024, 4100)])
 def test_plan_gemv_whole_tensor(hip, codec, shape):
