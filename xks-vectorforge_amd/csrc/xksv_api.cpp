@@ -657,6 +657,7 @@ int xksv_hip_plan_index(xksv_hip_plan* P, const void* archive, void* stream) {
       base[i + 1] = base[i] + segs * kMaxChunks * 64;
     }
     P->dindex_bytes = base.back() * sizeof(uint16_t);
+    if (P->dibase) (void)hipFree(P->dibase);  // left by a call whose index allocation failed
     if (!upload(base, &P->dibase)) return 1;
     if (hipMalloc(reinterpret_cast<void**>(&P->dindex), P->dindex_bytes) != hipSuccess) {
       P->dindex = nullptr;
