@@ -1924,7 +1924,14 @@ __device__ __forceinline__ const uint16_t* stream_index(const uint16_t* index, c
 
 // Decode XKSP2 blocks: one wave per block, its substreams in order, each
 // substream's inputs prefetched while the previous one decodes; the next
-// block's header is prefetched at the start of each block.
+// block's header is prefetched at the start of each block.  Blocks from
+// `split` on (the plan lists its largest blocks first, so these are its
+// smallest, one grid's worth) are claimed a quarter at a time -- substreams
+// [chunks q / 4, chunks (q + 1) / 4) -- so that the waves drain together:
+// a whole small block is ~0.3 ms of one wave's work, a quarter ~75 us.  Each
+// claim reports its block's header and stream errors into the block's status
+// word (an OR).
+constexpr uint32_t kTailSplit = 4;
 // kIdx: with a codeword index (a separate instantiation, so that the decode
 // without one compiles as if the indexed walk did not exist).
 template <bool kIdx>
@@ -1933,41 +1940,51 @@ k_decode_parallel(const DevBlock* __restrict__ blocks, uint32_t nblocks,
                                                         const uint8_t* __restrict__ arc, uint8_t* __restrict__ out,
                                                         uint32_t* __restrict__ status, uint32_t* queue,
                                                         const uint16_t* __restrict__ index,
-                                                        const uint64_t* __restrict__ ibase) {
+                                                        const uint64_t* __restrict__ ibase, uint32_t split) {
   __shared__ Smem S;
   const uint32_t lane = lane_id();
-  uint32_t b = blockIdx.x;
-  uint64_t hv = b < nblocks ? issue_head(arc + blocks[b].src, blocks[b].size, lane) : 0ull;
-  for (uint32_t bn; b < nblocks; b = bn) {
+  const uint32_t nclaims = split + (nblocks - split) * kTailSplit;
+  const auto block_of = [split](uint32_t c) { return c < split ? c : split + (c - split) / kTailSplit; };
+  uint32_t c = blockIdx.x;
+  uint64_t hv = c < nclaims ? issue_head(arc + blocks[block_of(c)].src, blocks[block_of(c)].size, lane) : 0ull;
+  for (uint32_t cn; c < nclaims; c = cn) {
+    const uint32_t b = block_of(c);
     const DevBlock d = blocks[b];
     const uint8_t* blk = arc + d.src;
     uint32_t chunks;
     uint32_t err = check_head(hv, d.size, d, lane, chunks);
     const uint64_t seglen_v = hv;
-    bn = claim_next(queue, b, lane);
-    if (bn < nblocks) hv = issue_head(arc + blocks[bn].src, blocks[bn].size, lane);
+    cn = claim_next(queue, c, lane);
+    if (cn < nclaims) hv = issue_head(arc + blocks[block_of(cn)].src, blocks[block_of(cn)].size, lane);
     if (err) {
       set_status(status, d.status_slot, err, lane);
       continue;
     }
+    const uint32_t q = c < split ? 0u : (c - split) % kTailSplit;
+    const uint32_t k0 = c < split ? 0u : chunks * q / kTailSplit;
+    const uint32_t k1 = c < split ? chunks : chunks * (q + 1) / kTailSplit;
+    if (k0 >= k1) continue;  // fewer than kTailSplit substreams: an empty quarter
     const uint64_t total = d.rows * d.cols;
     const bool aligned = d.rows % 16 == 0 && d.cols % 16 == 0;
     Writer C{out + d.dst, d.rows, d.cols, (uint32_t)(d.cols / 16), false};
+    // Substream k0's segment follows the header, the length table and the
+    // segments before it (lane 4 + j holds segment j's length).
     uint64_t off = 32 + 8ull * chunks;
-    uint64_t len = rdlane64(seglen_v, 4);
+    if (k0) off += rdlane64(wave_incl((uint64_t)(lane >= 4 && lane < 4 + k0 ? seglen_v : 0ull), lane), 63);
+    uint64_t len = rdlane64(seglen_v, 4 + k0);
     const uint32_t starts = substream_starts(total, chunks, lane);
     StreamIn PN;
-    issue_stream(PN, blk + off, blk + off + len, rdlane(starts, 1), lane);
+    issue_stream(PN, blk + off, blk + off + len, rdlane(starts, k0 + 1) - rdlane(starts, k0), lane);
     drain_loads();
     stage_inputs(S, lane, PN);
-    for (uint32_t k = 0; k < chunks && !err; ++k) {
+    for (uint32_t k = k0; k < k1 && !err; ++k) {
       const uint32_t s0 = rdlane(starts, k), s1 = rdlane(starts, k + 1);
       const uint64_t noff = off + len;
-      const uint64_t nlen = k + 1 < chunks ? rdlane64(seglen_v, 4 + k + 1) : 0ull;
-      const uint32_t ncount = k + 1 < chunks ? rdlane(starts, k + 2) - s1 : 0u;
+      const uint64_t nlen = k + 1 < k1 ? rdlane64(seglen_v, 4 + k + 1) : 0ull;
+      const uint32_t ncount = k + 1 < k1 ? rdlane(starts, k + 2) - s1 : 0u;
       C.aligned = aligned && unit_aligned(s0, s1 - s0, d.rows, d.cols);
       err = run_stream(S, lane, blk + off, blk + off + len, s1 - s0, s0, C,
-                       NextStream{k + 1 < chunks ? blk + noff : nullptr, blk + noff + nlen, ncount}, PN,
+                       NextStream{k + 1 < k1 ? blk + noff : nullptr, blk + noff + nlen, ncount}, PN,
                        kIdx ? stream_index(index, ibase, b, k, s1 - s0) : nullptr);
       off = noff;
       len = nlen;
@@ -2693,13 +2710,15 @@ hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t code
         hipLaunchKernelGGL(k_decode_items<false>, grid, blk, 0, s, blocks, nblocks, arc, out, status, index, ibase);
       return hipGetLastError();
     }
-    const dim3 grid(grid_for(nblocks, per_cu * cus));
+    // The last grid's worth of blocks is claimed by quarters (k_decode_parallel).
+    const uint32_t g = grid_for(nblocks, per_cu * cus);
+    const uint32_t split = nblocks > g ? nblocks - g : 0u;
     if (index)
-      hipLaunchKernelGGL(k_decode_parallel<true>, grid, blk, 0, s, blocks, nblocks, arc, out, status, queue, index,
-                         ibase);
+      hipLaunchKernelGGL(k_decode_parallel<true>, dim3(g), blk, 0, s, blocks, nblocks, arc, out, status, queue, index,
+                         ibase, split);
     else
-      hipLaunchKernelGGL(k_decode_parallel<false>, grid, blk, 0, s, blocks, nblocks, arc, out, status, queue, index,
-                         ibase);
+      hipLaunchKernelGGL(k_decode_parallel<false>, dim3(g), blk, 0, s, blocks, nblocks, arc, out, status, queue, index,
+                         ibase, split);
   } else {
     static const unsigned per_cu = groups_per_cu(k_decode_serial, 64);
     hipLaunchKernelGGL(k_decode_serial, dim3(grid_for(nblocks, per_cu * cus)), blk, 0, s, blocks, nblocks, arc, out,
