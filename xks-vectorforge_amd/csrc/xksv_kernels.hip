@@ -22,6 +22,12 @@
 // does not re-decodes from that exit.  A wave prefix sum places each lane's
 // symbols; the run is compacted in LDS and handed to a consumer (BF16 writer,
 // fused GEMV, fused GEMM) a whole 16x16 tile at a time.
+// With a codeword index (a load-time sidecar of static weights: the bit
+// offset of every 32nd codeword), lane l instead starts at the recorded
+// offset of symbol 32 l of each 2,048-symbol segment and decodes exactly 32
+// symbols into its own slot; the offsets are checked as they are used (every
+// lane must end where the next one starts), so an index that does not match
+// the stream only sends the segment back to the speculative path.
 // Streams with codes longer than 32 bits take a bit-serial path in the same
 // kernel.  Error semantics equal the reference's: a block fails iff the
 // reference's unpack fails on it.
