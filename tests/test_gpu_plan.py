@@ -301,6 +301,40 @@ def test_plan_gemm_nonstandard_chunk_counts(hip, oracle, batch):
         plan.close()
 
 
+def test_plan_decode_tail_quarters_few_substreams(hip, oracle):
+    """8,192 plan entries (one wave per block; the last grid's worth of blocks is claimed a
+    quarter at a time) over 16x1024 slabs re-split into 1, 2, 3, 5 and 32 substreams, so
+    some quarter claims hold no substream and others hold one or two; entry i decodes
+    slab i % 5 into its own output, one slab's code bits are damaged: exactly its entries
+    are reported and every other entry decodes exactly."""
+    counts = (1, 2, 3, 5, 32)
+    w = syn.normal_bf16(3100, (16 * len(counts), 1024))
+    blobs = [_resplit(hip, oracle, w[16 * i:16 * i + 16], c) for i, c in enumerate(counts)]
+    enc = np.frombuffer(b"".join(blobs), np.uint8).copy()
+    base = np.zeros(len(blobs), xksv_hip.BLOCK_DTYPE)
+    off = 0
+    for i, b in enumerate(blobs):
+        base[i] = (off, len(b), 32768, 0, 16, 1024, xksv_hip.CODEC_PARALLEL, 0)
+        off += len(b)
+    _corrupt_code_bits(oracle, enc, base[2])  # the 3-substream slab
+    n = 8192
+    table = np.resize(base, n).copy()
+    table["out_offset"] = np.arange(n, dtype=np.uint64) * 32768
+    d_arc = _upload(enc)
+    out = torch.zeros(n * 32768, dtype=torch.uint8, device="cuda")
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    try:
+        plan.decode(d_arc.data_ptr(), out.data_ptr(), out.numel())
+        nbad, first, bits = plan.errors()
+    finally:
+        plan.close()
+    bad = np.arange(n) % len(counts) == 2
+    assert (nbad, first, bits) == (int(bad.sum()), 2, xksv_hip.ERR_STREAM)
+    host = out.cpu().numpy().reshape(n, -1)
+    want = w.view(np.uint8).reshape(len(counts), -1)[np.arange(n) % len(counts)]
+    assert np.array_equal(host[~bad], want[~bad])
+
+
 @pytest.mark.parametrize("cols", [4096, 4112])
 @pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 16])
 def test_plan_gemm_staged_x(hip, batch, cols):
