@@ -1,17 +1,17 @@
-"""Three-symbol decode tables: fused GEMV/GEMM at batch 1 over slabs of 16,384+ columns (GPU only).
+"""Fused GEMV/GEMM at batch 1 over wide slabs (16,384 columns: substreams of 8,192 symbols), GPU only.
 
-Slabs that wide have substreams of 8,192+ symbols, and the fused batch-1 consumers
-(fp32 x and bf16 x) decode them with the engine's three-symbol table kind: up to three
-codes per 10-bit lookup, codes of 11-32 bits resolved inside the step, codes longer
-than 32 bits on the bit-serial path.  Narrower slabs and every other consumer keep the
-two-symbol tables.  These tests pin that walk to the oracle:
+Long substreams run many segments of the decode walk per stream, and the batch-1 VALU
+consumers (fp32 x) and the MFMA consumer (bf16 x) read them through both walks: the
+indexed walk (plan, codeword index built on the first call) and the speculative one
+(block API, no index; and wherever an index entry does not chain).  These tests pin both
+walks to the oracle on edge cases of the two-symbol lookup table:
 
-* crafted substreams, each from an explicit lengths table: 1-bit codes (three symbols
-  per lookup, streams ending inside an entry), codes of exactly the window's 10 bits,
-  codes of 11-31 bits, codes of up to 39 bits, flat 3-bit codes (three per lookup) and
-  flat 5-bit codes (two filling the window);
-* the plan (codeword index built on the first call: the indexed walk) and the block
-  API (no index: the speculative walk), fp32 and bf16 activations;
+* crafted substreams, each from an explicit lengths table: 1-bit codes (two symbols per
+  lookup, streams ending inside a pair), codes of exactly the window's 10 bits, codes of
+  11-31 bits resolved inside the step, codes of up to 39 bits (the bit-serial path), flat
+  3-bit codes (three fit the window, two are taken) and flat 5-bit codes (two filling the
+  window);
+* the plan (indexed walk) and the block API (speculative walk), fp32 and bf16 activations;
 * code bits changed after the index was built (a stale index: the segment that no
   longer chains continues speculatively), one change the oracle rejects and one it
   decodes to other weights;
@@ -35,7 +35,7 @@ from oracle_lib import craft_segment, raw_bytes
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
-COLS = 16384  # the narrowest slab width that takes the three-symbol tables
+COLS = 16384  # 16-row slabs of 16,384 columns: substreams of 8,192 symbols (4 index segments)
 
 
 def _rel_l2(got, want):
@@ -69,11 +69,11 @@ def _flat(bits: int, first: int) -> list:
 def _lengths(kind: str) -> list:
     """A complete lengths table; exponents stay between 2^-45 and 2^8 (finite BF16)."""
     lens = {
-        "one_bit": _chain(3, 124),   # 1, 2, 2: three codes per lookup, streams ending inside an entry
+        "one_bit": _chain(3, 124),   # 1, 2, 2: pairs of short codes, lanes ending inside a pair
         "ten_bit": _chain(11, 124),  # up to 10 bits: codes that fill the window exactly
         "long31": _chain(32, 124),   # up to 31 bits: long codes resolved inside the step
         "long40": _chain(40, 124),   # up to 39 bits: the bit-serial path
-        "flat3": _flat(3, 118),      # three 3-bit codes per lookup, the fourth never fits
+        "flat3": _flat(3, 118),      # 3-bit codes: three fit the window, a lookup takes two
         "flat5": _flat(5, 104),      # two 5-bit codes fill the 10-bit window exactly
     }[kind]
     assert abs(sum(2.0 ** -l for l in lens if l) - 1.0) < 1e-12
@@ -317,7 +317,7 @@ def test_plan_stale_index_wide(hip, oracle):
 
 def test_plan_unindexed_wide_items(hip, oracle):
     """High-entropy exponents (about 6 bits per code): segments too long for the index take
-    the speculative walk with the three-symbol tables; fp32 and bf16 x at batch 1."""
+    the speculative walk; fp32 and bf16 x at batch 1."""
     rows = 32
     rng = np.random.default_rng(91)
     w = ((rng.integers(64, 128, rows * COLS, dtype=np.uint32) << 7) | rng.integers(0, 256, rows * COLS, dtype=np.uint32))

@@ -235,9 +235,9 @@ int run_block_at(uint8_t* base, const BlockLayout& L, const uint8_t* input, uint
       const hipError_t e =
           mode == kGemmF32
               ? launch_gemm_f32(dd, 1, codec, base, static_cast<const float*>(x) + j0, batch, nb, y + j0, batch,
-                                status, items ? &is : nullptr, cus, cols, nullptr)
+                                status, items ? &is : nullptr, cus, nullptr)
               : launch_gemm_bf16(dd, 1, codec, base, static_cast<const uint16_t*>(x) + j0 * cols, cols, nb,
-                                 y + j0 * rows, rows, fused.tile, status, items ? &is : nullptr, cus, cols, nullptr);
+                                 y + j0 * rows, rows, fused.tile, status, items ? &is : nullptr, cus, nullptr);
       if (e != hipSuccess) return 1;
     }
   } else {
@@ -697,14 +697,14 @@ static int plan_gemm(xksv_hip_plan* P, const void* archive, const void* x, size_
     hipError_t e1, e2;
     if (!bf16) {
       e1 = launch_gemm_f32(P->g_fparallel, P->n_fparallel, kCodecParallel, arc, xf + j0, batch, nb, y + j0, batch,
-                           P->status, items, cus, P->cols, s);
+                           P->status, items, cus, s);
       e2 = launch_gemm_f32(P->g_fserial, P->n_fserial, kCodecSerial, arc, xf + j0, batch, nb, y + j0, batch,
-                           P->status, nullptr, cus, P->cols, s);
+                           P->status, nullptr, cus, s);
     } else {
       e1 = launch_gemm_bf16(P->g_fparallel, P->n_fparallel, kCodecParallel, arc, xb + j0 * K, K, nb, y + j0 * M, M,
-                            P->tile_parallel, P->status, items, cus, P->cols, s);
+                            P->tile_parallel, P->status, items, cus, s);
       e2 = launch_gemm_bf16(P->g_fserial, P->n_fserial, kCodecSerial, arc, xb + j0 * K, K, nb, y + j0 * M, M, true,
-                            P->status, nullptr, cus, P->cols, s);
+                            P->status, nullptr, cus, s);
     }
     if (e1 != hipSuccess || e2 != hipSuccess) return 1;
   }

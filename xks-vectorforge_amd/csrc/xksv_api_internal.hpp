@@ -63,18 +63,16 @@ hipError_t launch_decode(const DevBlock* blocks, uint32_t nblocks, uint32_t code
 uint64_t serial_wg_scratch(uint32_t nblocks, uint64_t max_elems, unsigned cus, uint32_t* grid, uint32_t* cap);
 hipError_t launch_decode_serial_wg(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint8_t* out,
                                    uint32_t* status, uint8_t* scratch, uint32_t cap, uint32_t grid, hipStream_t s);
-// `cols`: the slabs' column count (wide slabs at batch 1 take the
-// three-symbol decode tables).
 hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
-                           const ItemScratch* is, unsigned cus, uint64_t cols, hipStream_t s);
+                           const ItemScratch* is, unsigned cus, hipStream_t s);
 // bf16 X [batch rows of ldx], Y [batch rows of ldy]; bf16 MFMA when `mfma`
 // (every substream covers whole 16x16 tiles), VALU otherwise.
 // With `is` (scratch of kItemScratchPerBlock bytes per block, see
 // ItemScratch), XKSP2 blocks run by substream over every resident wave.
 hipError_t launch_gemm_bf16(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                             const uint16_t* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, bool mfma,
-                            uint32_t* status, const ItemScratch* is, unsigned cus, uint64_t cols, hipStream_t s);
+                            uint32_t* status, const ItemScratch* is, unsigned cus, hipStream_t s);
 hipError_t launch_copy_raw(const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc, uint8_t* out, hipStream_t s);
 hipError_t launch_gemm_plain(const DevBlock* blocks, uint32_t nblocks, const uint8_t* base, const float* x,
                              uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, hipStream_t s);

@@ -74,26 +74,10 @@ constexpr uint32_t kIdxMaxSpan = kStreamLanes * 128 - 7 - 96 - kLongLen - 32;
 // of the first code.  The two symbols sit in the bytes a byte store and a
 // high-half byte store write.  A window whose first code is longer than 10
 // bits (or matches no code) holds kLongMark; the step resolves it on the spot.
-//
-// Three-symbol entry (the table of the kL3 engine, for long streams): bits
-// 0-7 first symbol, 8-11 bits consumed, 12-13 symbols (1-3), 16-23 second and
-// 24-31 third symbol -- the codes that start in the window and end inside
-// it, at most three.  kLongEntry (no symbols) marks a window whose first code
-// is longer than 10 bits or matches no code.  Per lookup it takes ~2.9
-// symbols instead of ~2, for a third table read per entry when built: a net
-// gain on long streams (the fused GEMV/GEMM at batch 1 selects it for slabs
-// of 16,384 columns or more, substreams of 8,192+ symbols).
-constexpr uint32_t kLongEntry = 0;
 struct FastTables {
-  union {
-    uint32_t lut2[1u << kLutBits];
-    uint32_t lut3[1u << kLutBits];
-  };
+  uint32_t lut2[1u << kLutBits];
   uint64_t lim[40];              // lim[l] = left-aligned 32-bit end of the length-l codes, C(l+1)
-  union {
-    uint64_t slots[40];          // per-length lane masks (rank computation)
-    uint8_t slen[256];           // kL3: code length of each symbol, once the ranks are known
-  };
+  uint64_t slots[40];            // per-length lane masks (rank computation)
   uint32_t cnt[40];              // codes per length
   uint16_t base[40];             // index of the first length-l symbol in `sorted`
   uint16_t l4[16];               // codes of <= 4 bits, indexed by the top 4 bits
@@ -125,10 +109,10 @@ struct alignas(16) Smem {
   alignas(16) uint8_t syms[kSymsBytes];
 };
 // X columns of one indexed segment, staged for the fused GEMM consumers: in
-// the symbol buffer past the segment's symbols and the lanes' junk bytes.
-// Lane slots of the indexed walk: kIdxLaneSyms symbols, then padding that is
-// the lane's junk byte; 9 dwords, odd, so that lanes storing their n-th
-// symbol together hit distinct LDS banks.
+// the symbol buffer past the lane slots of the segment's symbols.
+// Lane slots of the indexed walk: kIdxLaneSyms symbols, then padding (a
+// lone symbol's second byte may land in it); 9 dwords, odd, so that lanes
+// storing their n-th symbol together hit distinct LDS banks.
 constexpr uint32_t kIdxStride = kIdxLaneSyms + 4;
 static_assert(kIdxStride % 8 == 4, "indexed lane slots: odd dword stride");
 constexpr uint32_t kXOff = kWave * kIdxStride;
@@ -327,7 +311,6 @@ struct Book {
 // C(l) = first code of length l; a symbol's code is C(l) + rank * 2^(32-l),
 // rank = number of smaller symbols of the same length.  The assignment is
 // oversubscribed (the reference throws) iff the Kraft total exceeds 2^32.
-template <bool kL3 = false>
 __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, uint32_t L1, uint32_t L2, uint32_t L3,
                            uint32_t maxlen) {
   FastTables& F = S.t.f;
@@ -375,9 +358,6 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
     }
   }
   wave_sync();
-  // kL3: the rank masks are dead; their space holds each symbol's code length
-  // (read where a walk ends inside a three-symbol entry).
-  if constexpr (kL3) reinterpret_cast<uint32_t*>(F.slen)[lane] = L0 | (L1 << 8) | (L2 << 16) | (L3 << 24);
   // Per-length group sums: C(l+1) = sum_{l' <= l} cnt[l'] * 2^(32 - l').
   const uint32_t c = (lane >= 1 && lane <= 32) ? F.cnt[lane] : 0u;
   const uint64_t g = (lane >= 1 && lane <= 32) ? ((uint64_t)c << (32 - lane)) : 0ull;
@@ -465,41 +445,6 @@ __device__ __forceinline__ Book build_fast(Smem& S, uint32_t lane, uint32_t L0, 
   wave_sync();
   const uint32_t* lut1r = lut1;
   const uint32_t lane_hi = lane << 26;
-  if constexpr (kL3) {
-    // Three-symbol table: entry e holds its first code and, while they also
-    // end within the 10-bit window, the next one or two.  Lane l takes
-    // entries l + 64 i.  A later code is read at the window shifted past the
-    // codes before it, with the lane's top bits as fill (as below, s = the
-    // shift; a marker has s = 0 and its fill is masked off).
-    constexpr uint32_t kMask = (1u << kLutBits) - 1;
-#pragma unroll
-    for (uint32_t g = 0; g < 2; ++g) {  // eight entries at a time: three LDS round trips per group
-      uint32_t v1[8], v2[8], v3[8];
-#pragma unroll
-      for (uint32_t i = 0; i < 8; ++i) v1[i] = lut1r[lane + kWave * (8 * g + i)];
-#pragma unroll
-      for (uint32_t i = 0; i < 8; ++i) {
-        const uint32_t sh = v1[i] >> 28;
-        v2[i] = lut1r[(((lane + kWave * (8 * g + i)) << sh) | __builtin_amdgcn_alignbit(0u, lane_hi, 32u - sh)) & kMask];
-      }
-#pragma unroll
-      for (uint32_t i = 0; i < 8; ++i) {
-        const uint32_t sh = (v1[i] >> 28) + (v2[i] >> 28);  // at most 20
-        v3[i] = lut1r[(((lane + kWave * (8 * g + i)) << sh) | __builtin_amdgcn_alignbit(0u, lane_hi, 32u - sh)) & kMask];
-      }
-#pragma unroll
-      for (uint32_t i = 0; i < 8; ++i) {
-        const uint32_t l1 = (v1[i] >> 8) & 127u, l2 = (v2[i] >> 8) & 127u, l3 = (v3[i] >> 8) & 127u;
-        const bool two = l1 + l2 <= kLutBits, three = two && l1 + l2 + l3 <= kLutBits;
-        const uint32_t n = 1u + two + three, cons = l1 + (two ? l2 : 0u) + (three ? l3 : 0u);
-        const uint32_t e =
-            (v1[i] & 255u) | (cons << 8) | (n << 12) | ((v2[i] & 255u) << 16) | ((v3[i] & 255u) << 24);
-        F.lut3[lane + kWave * (8 * g + i)] = l1 <= kLutBits ? e : kLongEntry;
-      }
-    }
-    wave_sync();
-    return Book{0, maxlen, true};
-  }
   // Two-symbol table: entry e holds its first code and, when the code after
   // it also ends within the 10-bit window, that one too.  Lane l takes
   // entries l + 64 i (consecutive lanes, consecutive words).  With the
@@ -581,13 +526,12 @@ __device__ __forceinline__ Book build_slow(Smem& S, uint32_t lane, uint32_t lw, 
 }
 
 // `lw` holds the code lengths of symbols 4 lane .. 4 lane + 3.
-template <bool kL3 = false>
 __device__ __forceinline__ Book build_book(Smem& S, uint32_t lane, uint32_t lw) {
   const uint32_t L0 = lw & 255u, L1 = (lw >> 8) & 255u, L2 = (lw >> 16) & 255u, L3 = lw >> 24;
   const uint32_t mx = max(max(L0, L1), max(L2, L3));
   const uint32_t maxlen = wave_max(mx);
   if (maxlen > kMaxLenFast) return build_slow(S, lane, lw, maxlen);
-  return build_fast<kL3>(S, lane, L0, L1, L2, L3, maxlen);
+  return build_fast(S, lane, L0, L1, L2, L3, maxlen);
 }
 
 // ---------------------------------------------------------------- decode
@@ -669,42 +613,6 @@ __device__ __forceinline__ uint32_t end_pair(uint32_t le, uint32_t end, uint32_t
   return back;
 }
 
-// Up to three codewords at bit p (three-symbol entries), as step2; `adv` =
-// the bits they take.  A dead window advances kLongLen bits.  Later
-// codewords of the entry may start at or past the caller's end; the caller
-// undoes that after its last step (end_fix).
-__device__ __forceinline__ uint32_t step3(const Smem& S, uint32_t& p, uint32_t& wi, uint32_t& w0, uint32_t& w1,
-                                          uint32_t& w2, uint32_t maxlen, uint32_t& dead, uint32_t& adv) {
-  const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, 0u - p);
-  uint32_t e = S.t.f.lut3[win >> (32 - kLutBits)];
-  adv = (e >> 8) & 15u;
-  if (__builtin_expect(__ballot(e == kLongEntry) != 0, 0)) {
-    if (e == kLongEntry) {
-      const uint32_t lc = long_code(S, win, maxlen);  // (len << 8) | symbol
-      dead |= lc == 0;
-      adv = lc ? lc >> 8 : kLongLen;
-      e = (lc & 255u) | (1u << 12);
-    }
-  }
-  p += adv;
-  slide(S, p, wi, w0, w1, w2);
-  return e;
-}
-
-// After a loop of step3 calls that stopped at the first p >= end, with `le`
-// / `adv` the last step's entry and advance: the entry's later codewords that
-// start at or past `end` belong to the next range: step back to the first of
-// them.  Returns how many symbols were taken back.
-__device__ __forceinline__ uint32_t end_fix(const Smem& S, uint32_t le, uint32_t adv, uint32_t end, uint32_t& p) {
-  const uint32_t n = (le >> 12) & 3u;
-  if (n < 2) return 0;
-  const uint32_t t2 = p - adv + S.t.f.slen[le & 255u];
-  const uint32_t t3 = t2 + S.t.f.slen[(le >> 16) & 255u];
-  const uint32_t back = t2 >= end ? n - 1 : (n == 3 && t3 >= end ? 1u : 0u);
-  p = back == n - 1 ? t2 : back ? t3 : p;
-  return back;
-}
-
 __device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t& wb, uint32_t& w0, uint32_t& w1,
                                             uint32_t& w2) {
   const uint32_t j = (p + 31) >> 5;
@@ -722,19 +630,13 @@ __device__ __forceinline__ void load_window(const Smem& S, uint32_t p, uint32_t&
 // lane's exit).  Symbols are stored a byte at a time (aligned LDS stores).
 // A path that meets a window matching no code is dead: it produces no start
 // (f = kNoStart) when that happens before cs, and its symbols are never used.
-template <bool kL3 = false>
 __device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint32_t cs, uint32_t ce, uint8_t* region,
                                              uint32_t maxlen, Path& P) {
-  uint32_t p = from, d = 0, wi, w0, w1, w2, le = 0, adv = 0;
+  uint32_t p = from, d = 0, wi, w0, w1, w2, le = 0;
   load_window(S, p, wi, w0, w1, w2);
   if (p < cs) {
-    if constexpr (kL3) {
-      while (p < cs) le = step3(S, p, wi, w0, w1, w2, maxlen, d, adv);
-      end_fix(S, le, adv, cs, p);
-    } else {
-      while (p < cs) le = step2(S, p, wi, w0, w1, w2, maxlen, d);
-      end_pair(le, cs, p);
-    }
+    while (p < cs) le = step2(S, p, wi, w0, w1, w2, maxlen, d);
+    end_pair(le, cs, p);
     load_window(S, p, wi, w0, w1, w2);
   }
   P.f = d ? kNoStart : p;
@@ -742,16 +644,7 @@ __device__ __forceinline__ void decode_chunk(const Smem& S, uint32_t from, uint3
   lds_bytes const out = as_lds(region);
   lds_bytes o = out;  // next symbol slot
   le = 0;
-  if constexpr (kL3) {
-    while (p < ce) {
-      le = step3(S, p, wi, w0, w1, w2, maxlen, d, adv);
-      o[0] = (uint8_t)le;  // all three bytes: the region has room past the last symbol
-      o[1] = (uint8_t)(le >> 16);
-      o[2] = (uint8_t)(le >> 24);
-      o += (le >> 12) & 3u;
-    }
-    P.cnt = (uint32_t)(o - out) - end_fix(S, le, adv, ce, p);
-  } else {
+  {
     while (p < ce) {
       le = step2(S, p, wi, w0, w1, w2, maxlen, d);
       o[0] = (uint8_t)le;
@@ -897,7 +790,7 @@ struct SmUse {
 // Decode one stream with the fast tables; the consumer receives the
 // exponents in stream order.  `first` holds the stream's first 784 code
 // bytes; later segments are loaded one segment ahead.  Returns error bits.
-template <class Cons, bool kL3 = false>
+template <class Cons>
 //
 // `start_bit` / `start_pos` resume the stream at a codeword boundary already
 // known to be true (its symbol index start_pos, a multiple of 256): the
@@ -961,7 +854,7 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
     // when that is closer.  An inactive lane's empty range gives f = ex = cs,
     // cnt = 0.
     Path P;
-    decode_chunk<kL3>(S, !active ? cs : lane == 0 ? (spec ? 0u : entry) : cs > entry + kSync ? cs - kSync : entry, cs, ce,
+    decode_chunk(S, !active ? cs : lane == 0 ? (spec ? 0u : entry) : cs > entry + kSync ? cs - kSync : entry, cs, ce,
                  region, maxlen, P);
     if (spec) {  // the range's first codeword on lane 0's path: trusted here, checked by the caller
       const uint32_t f0 = rdlane(P.f, 0);
@@ -993,7 +886,7 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
       if (!bad) break;
       const bool redo = !ok && !pd;
       Path Q;
-      decode_chunk<kL3>(S, redo ? pe : ce, redo ? cs : ce, ce, region, maxlen, Q);  // empty range unless redo
+      decode_chunk(S, redo ? pe : ce, redo ? cs : ce, ce, region, maxlen, Q);  // empty range unless redo
       if (redo) P = Q;
     }
     if (err) break;
@@ -1128,7 +1021,7 @@ __device__ __forceinline__ uint32_t decode_fast(Smem& S, uint32_t lane, const St
 // The entries are read from LDS (kIxOff): segment 0's are copied there by
 // the caller while the tables are built, each later segment's one segment
 // ahead, so no segment waits on them.
-template <class Cons, bool kL3 = false>
+template <class Cons>
 __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Stream& st, uint32_t maxlen,
                                                const uint8_t* blk_end, Cons& C, const StreamIn& PN, bool next,
                                                const uint16_t* idx, uint32_t& err, uint64_t& rbit, uint32_t& rpos) {
@@ -1177,39 +1070,11 @@ __device__ __forceinline__ bool decode_indexed(Smem& S, uint32_t lane, const Str
     uint32_t p = base + rel, n = 0, d = 0, wi, w0, w1, w2;
     load_window(S, p, wi, w0, w1, w2);
     lds_bytes const o = as_lds(S.syms + kIdxStride * lane);
-    // In the three-symbol tail, a symbol the lane does not want (past its k)
-    // is stored into the lane's own junk byte past its symbols (the slot's
-    // padding), so the step has no branch around the store.
-    lds_bytes const junk = o + kIdxLaneSyms;
     // One exit condition: a lane walks exactly k symbols.  A path on wrong
     // offsets (a stale index) advances at most 127 bits per step for at most
     // kIdxLaneSyms steps, which stays inside this wave's LDS block, and fails
     // the check below.
-    if constexpr (kL3) {
-      // Steps that cannot pass k store all three bytes (the slots past a
-      // step's last symbol are rewritten by the next step); the last step or
-      // two store only what is wanted and step the position back to the
-      // first dropped codeword.
-      uint32_t adv;
-      while (n + 3 <= k) {
-        const uint32_t en = step3(S, p, wi, w0, w1, w2, maxlen, d, adv);
-        o[n] = (uint8_t)en;
-        o[n + 1] = (uint8_t)(en >> 16);
-        o[n + 2] = (uint8_t)(en >> 24);
-        n += (en >> 12) & 3u;
-      }
-      while (n < k) {  // at most two symbols left
-        const uint32_t en = step3(S, p, wi, w0, w1, w2, maxlen, d, adv);
-        const uint32_t ne = (en >> 12) & 3u, take = min(ne, k - n);
-        o[n] = (uint8_t)en;
-        (take >= 2 ? o + n + 1 : junk)[0] = (uint8_t)(en >> 16);
-        if (take < ne) {  // the lane's run ends inside this entry
-          const uint32_t t2 = p - adv + S.t.f.slen[en & 255u];
-          p = take == 1 ? t2 : t2 + S.t.f.slen[(en >> 16) & 255u];
-        }
-        n += take;
-      }
-    } else {
+    {
       // Steps that cannot pass k store both bytes (a lone symbol's second
       // byte is rewritten by the next step); a last single symbol takes one
       // more step that keeps only the entry's first code.  Four steps per
@@ -1348,7 +1213,7 @@ __device__ __forceinline__ uint32_t fail_stream(Smem& S, uint32_t lane, uint32_t
 // The next stream's inputs are issued once this stream's header and lengths
 // are in use: loads complete in issue order, so a wait for them issued after
 // the prefetch would wait for the prefetch too.
-template <class Cons, bool kL3 = false>
+template <class Cons>
 __device__ __forceinline__ uint32_t stream_body(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end,
                                                 uint32_t count, uint32_t start, Cons& C, const NextStream& N,
                                                 StreamIn& PN, const uint16_t* idx) {
@@ -1369,16 +1234,16 @@ __device__ __forceinline__ uint32_t stream_body(Smem& S, uint32_t lane, const ui
   st.nbits = nb;
   st.count = count;
   st.start = start;
-  const Book b = build_book<kL3>(S, lane, lw);
+  const Book b = build_book(S, lane, lw);
   if (idx) drain_loads();
   if (b.err) return fail_stream(S, lane, b.err, N, PN);
   if (!b.fast) return decode_slow(S, lane, st, C, PN, N.seg);
   uint64_t rbit = 0;
   uint32_t rpos = 0, err = 0;
   if (idx && reinterpret_cast<const uint16_t*>(S.syms + kIxOff)[0] != kIdxNone &&
-      decode_indexed<Cons, kL3>(S, lane, st, b.maxlen, seg_end, C, PN, N.seg, idx, err, rbit, rpos))
+      decode_indexed<Cons>(S, lane, st, b.maxlen, seg_end, C, PN, N.seg, idx, err, rbit, rpos))
     return err;
-  return decode_fast<Cons, kL3>(S, lane, st, b.maxlen, seg_end, C, PN, N.seg, rbit, rpos);
+  return decode_fast<Cons>(S, lane, st, b.maxlen, seg_end, C, PN, N.seg, rbit, rpos);
 }
 
 // One stream whose inputs were staged in LDS (stage_inputs); the next
@@ -1386,11 +1251,11 @@ __device__ __forceinline__ uint32_t stream_body(Smem& S, uint32_t lane, const ui
 // load while this stream decodes, and staged when it finishes.  A stream that
 // fails before its last segment stages them on the way out.  `idx`: the
 // stream's codeword index (fused GEMM items), or nullptr.
-template <class Cons, bool kL3 = false>
+template <class Cons>
 __device__ __forceinline__ uint32_t run_stream(Smem& S, uint32_t lane, const uint8_t* seg, const uint8_t* seg_end,
                                                uint32_t count, uint32_t start, Cons& C, const NextStream& N,
                                                StreamIn& PN, const uint16_t* idx = nullptr) {
-  return stream_body<Cons, kL3>(S, lane, seg, seg_end, count, start, C, N, PN, idx);
+  return stream_body<Cons>(S, lane, seg, seg_end, count, start, C, N, PN, idx);
 }
 
 // ------------------------------------------------------------- consumers
@@ -2366,7 +2231,7 @@ k_decode_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint
 // records in order and stores its status word, so no status reset precedes
 // the launch.  The next item's inputs and the header of the one after load
 // while an item decodes.
-template <class Acc, bool kL3 = false>
+template <class Acc>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
 k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_t* __restrict__ arc, GemmArgs ga,
              ItemScratch is) {
@@ -2403,7 +2268,7 @@ k_gemm_items(const DevBlock* __restrict__ blocks, uint32_t nblocks, const uint8_
       // (an item with more symbols than its allotment holds has no index entry)
       const uint16_t* idx =
           is.index && L.count <= is.index_segs * kIdxSegSyms ? is.index + (uint64_t)i * is.index_segs * 64 : nullptr;
-      err = run_stream<Acc, kL3>(S, lane, L.seg, L.end, L.count, L.s0, C,
+      err = run_stream<Acc>(S, lane, L.seg, L.end, L.count, L.s0, C,
                                  NextStream{LN.run ? LN.seg : nullptr, LN.end, LN.count}, PN, idx);
       // Live batch columns only, packed: row r, column j < nb at r * nb + j;
       // every output of the item sits in one lane, which stores it.
@@ -2783,37 +2648,31 @@ static void gemm_launch(hipStream_t s, const DevBlock* blocks, uint32_t nblocks,
 
 // Item-scheduled launch (XKSP2 blocks with item scratch): the item kernel
 // over all resident waves, then the in-order reduction.
-template <class Acc, bool kL3 = false>
+template <class Acc>
 static void items_launch(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, const uint8_t* arc,
                          const GemmArgs& ga, uint32_t* status, const ItemScratch& is, unsigned cus) {
-  static const unsigned per_cu = groups_per_cu(k_gemm_items<Acc, kL3>, 64);
-  hipLaunchKernelGGL((k_gemm_items<Acc, kL3>), dim3(grid_for((uint64_t)nblocks * kMaxChunks, per_cu * cus)), dim3(64),
+  static const unsigned per_cu = groups_per_cu(k_gemm_items<Acc>, 64);
+  hipLaunchKernelGGL((k_gemm_items<Acc>), dim3(grid_for((uint64_t)nblocks * kMaxChunks, per_cu * cus)), dim3(64),
                      0, s, blocks, nblocks, arc, ga, is);
   hipLaunchKernelGGL((k_gemm_finish<Acc>), dim3(grid_for(nblocks, 8 * cus)), dim3(64), 0, s, blocks, nblocks, ga,
                      status, is);
 }
 
-// XKSP2 blocks: by substream when item scratch is given (kL3: the
-// three-symbol tables), else one workgroup of 4 waves per block (substreams
-// split over the waves).  Serial blocks: one wave per block.
-template <class Acc, bool kL3 = false>
+// XKSP2 blocks: by substream when item scratch is given, else one workgroup
+// of 4 waves per block (substreams split over the waves).  Serial blocks: one
+// wave per block.
+template <class Acc>
 static void gemm_any(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                      const GemmArgs& ga, uint32_t* status, const ItemScratch* is, unsigned cus) {
-  if (codec == kCodecParallel && is) items_launch<Acc, kL3>(s, blocks, nblocks, arc, ga, status, *is, cus);
+  if (codec == kCodecParallel && is) items_launch<Acc>(s, blocks, nblocks, arc, ga, status, *is, cus);
   else if (codec == kCodecParallel) gemm_launch<4, Acc>(s, blocks, nblocks, codec, arc, ga, status, cus);
   else gemm_launch<1, Acc>(s, blocks, nblocks, codec, arc, ga, status, cus);
 }
 
-// `wide`: slabs of kL3Cols columns or more, whose substreams are long enough
-// for the three-symbol tables to pay (batch 1; measured against the
-// two-symbol walk: 8192 x 28672 bf16 GEMM -3.5 %; at 14,336 columns even, at
-// 8,192 +6 %, at 4,096 +6 %).
-constexpr uint64_t kL3Cols = 16384;
 template <template <int> class Acc>
 static void gemm_valu(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
-                      const GemmArgs& ga, uint32_t* status, const ItemScratch* is, unsigned cus, bool wide) {
-  if (ga.nb == 1 && wide) gemm_any<Acc<1>, true>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
-  else if (ga.nb == 1) gemm_any<Acc<1>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
+                      const GemmArgs& ga, uint32_t* status, const ItemScratch* is, unsigned cus) {
+  if (ga.nb == 1) gemm_any<Acc<1>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   else if (ga.nb <= 4) gemm_any<Acc<4>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   else if (ga.nb <= 8) gemm_any<Acc<8>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   else gemm_any<Acc<16>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
@@ -2821,24 +2680,24 @@ static void gemm_valu(hipStream_t s, const DevBlock* blocks, uint32_t nblocks, u
 
 hipError_t launch_gemm_f32(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                            const float* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, uint32_t* status,
-                           const ItemScratch* is, unsigned cus, uint64_t cols, hipStream_t s) {
+                           const ItemScratch* is, unsigned cus, hipStream_t s) {
   if (!nblocks) return hipSuccess;
   const GemmArgs ga{x, ldx, nb, y, ldy};
   // GemmF32<1> reads x as a contiguous vector; a one-column group of a wider
   // X (the last group of a batch of 16 k + 1) takes the strided consumer.
   if (nb == 1 && ldx != 1) gemm_any<GemmF32<4>>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
-  else gemm_valu<GemmF32>(s, blocks, nblocks, codec, arc, ga, status, is, cus, cols >= kL3Cols);
+  else gemm_valu<GemmF32>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   return hipGetLastError();
 }
 
 hipError_t launch_gemm_bf16(const DevBlock* blocks, uint32_t nblocks, uint32_t codec, const uint8_t* arc,
                             const uint16_t* x, uint64_t ldx, uint32_t nb, float* y, uint64_t ldy, bool mfma,
-                            uint32_t* status, const ItemScratch* is, unsigned cus, uint64_t cols, hipStream_t s) {
+                            uint32_t* status, const ItemScratch* is, unsigned cus, hipStream_t s) {
   if (!nblocks) return hipSuccess;
   const GemmArgs ga{x, ldx, nb, y, ldy};
   // MFMA at every batch (batch 1 padded: 2-3 % faster than the VALU consumer at the 70B shapes)
   if (mfma) gemm_any<GemmMfma>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
-  else gemm_valu<GemmBf16>(s, blocks, nblocks, codec, arc, ga, status, is, cus, cols >= kL3Cols);
+  else gemm_valu<GemmBf16>(s, blocks, nblocks, codec, arc, ga, status, is, cus);
   return hipGetLastError();
 }
 
