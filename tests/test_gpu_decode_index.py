@@ -197,3 +197,33 @@ def test_index_without_parallel_blocks(hip):
         assert errs[0] == 0 and host.tobytes() == raw_bytes(w)
     finally:
         plan.close()
+
+
+def test_index_and_gemm_on_one_plan(hip, oracle):
+    """A decode plan with the decode index and a GEMM plan over the same archive (whose fused
+    GEMMs build their own index on the first call, and which then gets a decode index too):
+    decodes and GEMVs interleaved stay exact."""
+    rows, cols = 64, 4096
+    w = syn.normal_bf16(190, (rows, cols))
+    enc, table = hip.encode_tensor(w, 2)
+    d_arc = _upload(enc)
+    plan = xksv_hip.Plan(hip, table, enc.nbytes)
+    gtable = table.copy()
+    gtable["out_offset"] //= cols * 2
+    gplan = xksv_hip.Plan(hip, gtable, enc.nbytes)
+    try:
+        plan.index(d_arc.data_ptr())
+        x = torch.randn(cols, device="cuda")
+        want_y = oracle.gemm_f64(w, x.cpu().numpy().astype(np.float64))
+        for _ in range(2):
+            host, errs = _decode(plan, d_arc, w.nbytes)
+            assert errs[0] == 0 and host.tobytes() == raw_bytes(w)
+            y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+            gplan.gemm(d_arc.data_ptr(), x.data_ptr(), 1, y.data_ptr())
+            assert gplan.errors()[0] == 0
+            got = y.cpu().numpy().astype(np.float64)
+            assert np.linalg.norm(got - want_y) <= 1e-5 * np.linalg.norm(want_y)
+            gplan.index(d_arc.data_ptr())  # a decode index on the GEMM plan too: GEMMs unaffected
+    finally:
+        plan.close()
+        gplan.close()
